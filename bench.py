@@ -1,0 +1,322 @@
+"""Benchmark: QuaternionMamba2Block forward on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--mode full|ssm|cumprod|qln|copy]
+
+Workload (BASELINE configs[2]/[3] shape): one QuaternionMamba2Block forward,
+batch 4, seq_len 2048, d_model 768, d_state 64, d_conv 4, expand_factor 2
+(d_inner 1536); random-init weights (seed 0), bf16 storage with fp32
+accumulation in the HIP kernels, synthetic x ~ N(0, 1) resident in HBM.
+
+`value` is block-forward tokens/s (batch*seq_len*steps / timed seconds,
+timed region bracketed by torch.cuda.synchronize()). `roofline` is the fused
+SSM kernel (mqc_ssm_fused_fwd): algorithmic bytes per launch divided by its
+mean launch duration, measured with HIP events on the stream it runs on.
+`cpu_baseline` times the CPU oracle (a restatement of the reference's
+sequential torch path) on a bounded prefix of the same workload.
+
+The other modes run one kernel in a loop for rocprofv3 (no JSON contract).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "block fwd tokens/s @B4 T2048 d768 s64; scan HBM GB/s as % of peak"
+PEAK_HBM_GBS = 8000.0
+B, T, DM, DS, DCONV, EXPAND = 4, 2048, 768, 64, 4, 2
+DI = DM * EXPAND
+
+
+def ssm_bytes(b, t, d, s, el=2):
+    """Algorithmic HBM bytes of one fused SSM launch: B and C read once,
+    delta and s read once, Lambda (fp32, 4 per (d,k)) and D (fp32) read once,
+    y written once."""
+    return (2 * b * t * d * s * 4 * el + 2 * b * t * d * el + d * s * 4 * 4 + d * 4
+            + b * t * d * 4 * el)
+
+
+def qln_bytes(rows, d, el=2):
+    return 2 * rows * d * 4 * el + d * 4 + d * 16
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def event_time_ms(fn, reps):
+    """Mean duration of fn() over reps launches, each bracketed by events on the
+    current stream (the stream the library launches on)."""
+    import torch
+
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    for i in range(reps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / reps
+
+
+def make_block(dtype):
+    import torch
+    import mambaqc_amd
+
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        blk = mambaqc_amd.QuaternionMamba2Block(DM, d_state=DS, d_conv=DCONV, expand_factor=EXPAND)
+    return blk.to(dtype).eval()
+
+
+def ssm_inputs(blk, x):
+    """The fused SSM's operands exactly as the block forms them for input x."""
+    import torch
+    import torch.nn.functional as F
+
+    with torch.no_grad():
+        xz = blk.in_proj(x)
+        x_in, _ = xz.chunk(2, dim=-1)
+        xa = F.silu(blk.conv1d(x_in))
+        delta = F.softplus(blk.dt_proj(xa))
+        Bq = blk.B_proj(xa).view(B, T, DI, DS, 4)
+        Cq = blk.C_proj(xa).view(B, T, DI, DS, 4)
+        s = torch.sigmoid(blk.gate_proj(xa)) * xa
+    return delta, s, Bq, Cq
+
+
+def cpu_baseline(blk, x, t_sample=128):
+    """Oracle block forward (fp32, CPU) on the first t_sample steps of the same
+    input, with the same weights. The sequential path's cost is linear in T."""
+    import torch
+    import oracle
+
+    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16")))
+    torch.set_num_threads(threads)
+    sd = {k: v.detach().float().cpu() for k, v in blk.state_dict().items()}
+    xs = x[:, :t_sample].float().cpu()
+    oracle.block_forward_reference(sd, xs[:, :2], d_state=DS)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.block_forward_reference(sd, xs, d_state=DS)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[1]
+    cpu = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(B * t_sample / med, 2),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle block forward (fp32 torch restatement of the reference's sequential "
+                   f"CPU path) on x[:, :{t_sample}] of the B4 d768 s64 workload, median of 3; "
+                   f"os.cpu_count()={os.cpu_count()}, cpu={cpu}"),
+    }
+
+
+def read_traffic():
+    """HBM bytes per launch of the SSM kernel from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor)."""
+    p = ROOT / "profiles" / "ssm_fused_fwd_c3_traffic.txt"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def run_full(args):
+    import torch
+    from mambaqc_amd import kernels as K
+
+    dtype = torch.bfloat16
+    log(f"building block d_model={DM} d_state={DS} expand={EXPAND} on {torch.cuda.get_device_name(0)}")
+    blk = make_block(dtype)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(B, T, DM, generator=g, device="cuda").to(dtype)
+
+    with torch.inference_mode():
+        for i in range(args.warmup):
+            blk(x)
+        torch.cuda.synchronize()
+        log(f"warmup {args.warmup} done")
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            out = blk(x)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    ms_step = elapsed * 1e3 / args.steps
+    tokens_s = B * T * args.steps / elapsed
+    log(f"block fwd: {ms_step:.3f} ms/step, {tokens_s:.0f} tokens/s")
+
+    # Fused SSM kernel alone, on the block's own operands.
+    delta, s, Bq, Cq = ssm_inputs(blk, x)
+    la, li, Dv = (blk.Lambda_alpha.detach().float(), blk.Lambda_imag.detach().float(),
+                  blk.D.detach().float())
+    fn = lambda: K.ssm_forward_fused_dl(delta, s, Bq, Cq, la, li, Dv, eps=1e-6)
+    with torch.inference_mode():
+        fn()
+        ssm_ms = event_time_ms(fn, max(args.steps, 10))
+    nbytes = ssm_bytes(B, T, DI, DS)
+    achieved = nbytes / (ssm_ms * 1e-3) / 1e9
+    log(f"ssm_fused_fwd: {ssm_ms:.3f} ms, {achieved:.0f} GB/s ({achieved / PEAK_HBM_GBS:.1%} of 8 TB/s)")
+
+    # Per-stage breakdown of one block forward (events around each stage).
+    stages = {}
+    with torch.inference_mode():
+        y = fn()
+        stages["ssm_fused_fwd"] = ssm_ms
+        stages["qln"] = event_time_ms(lambda: blk.norm(y), 10)
+        stages["B_proj+C_proj GEMMs"] = event_time_ms(lambda: (blk.B_proj(s), blk.C_proj(s)), 5)
+        del y
+    qln_gbs = qln_bytes(B * T, DI) / (stages["qln"] * 1e-3) / 1e9
+    del delta, s, Bq, Cq
+    torch.cuda.empty_cache()
+
+    # Config 2 standalone: Cayley then cumprod, fp32 [2,256,768,64,4].
+    shape = (2, 256, 768, 64)
+    z = torch.empty(*shape, 4, device="cuda")
+    n = lambda: torch.randn(*shape, generator=g, device="cuda")
+    z[..., 0] = -torch.exp(n()) * torch.nn.functional.softplus(n())
+    for c in range(1, 4):
+        z[..., c] = n() * torch.nn.functional.softplus(n())
+    with torch.inference_mode():
+        q = K.cayley_discretization_fused(z)
+        cay_ms = event_time_ms(lambda: K.cayley_discretization_fused(z), 10)
+        K.parallel_scan_quaternion(q)
+        scan_ms = event_time_ms(lambda: K.parallel_scan_quaternion(q), 10)
+    c2_bytes = 2 * z.numel() * 4
+    del z, q
+    torch.cuda.empty_cache()
+
+    base = None if args.no_cpu else cpu_baseline(blk, x)
+    if base:
+        log(f"cpu baseline: {base['value']} tokens/s on {base['cores']} threads")
+
+    result = {
+        "metric": METRIC,
+        "value": round(tokens_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (x ~ N(0,1), random-init weights seed 0)",
+        "config": {
+            "workload": "QuaternionMamba2Block forward, bf16 storage / fp32 accumulate",
+            "global_batch": B, "seq_len": T, "d_model": DM, "d_state": DS, "d_conv": DCONV,
+            "expand_factor": EXPAND, "d_inner": DI, "parallelism": "single GPU",
+        },
+        "roofline": {
+            "kernel": "mqc_ssm_fused_fwd (ssm_scan_kernel<bf16, delta-lambda>)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": read_traffic(),
+            "algorithmic_bytes": nbytes,
+            "mean_launch_ms": round(ssm_ms, 4),
+        },
+        "stages_ms": {k: round(v, 4) for k, v in stages.items()},
+        "components": {
+            "qln_c3_GBs": round(qln_gbs, 1),
+            "cayley_c2_GBs": round(c2_bytes / (cay_ms * 1e-3) / 1e9, 1),
+            "cumprod_scan_c2_GBs": round(c2_bytes / (scan_ms * 1e-3) / 1e9, 1),
+            "cayley_c2_ms": round(cay_ms, 4),
+            "cumprod_scan_c2_ms": round(scan_ms, 4),
+        },
+        "cpu_baseline": base,
+    }
+    print(json.dumps(result), flush=True)
+
+
+def run_kernel_loop(args):
+    """One kernel in a loop (for rocprofv3 kernel traces and PMC passes)."""
+    import torch
+    from mambaqc_amd import kernels as K
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    reps = args.steps
+    with torch.inference_mode():
+        if args.mode == "ssm":
+            bf = torch.bfloat16
+            delta = torch.nn.functional.softplus(torch.randn(B, T, DI, generator=g, device="cuda") - 2).to(bf)
+            s = torch.randn(B, T, DI, generator=g, device="cuda").to(bf)
+            Bq = torch.randn(B, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
+            Cq = torch.randn(B, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
+            la = torch.randn(DI, DS, generator=g, device="cuda") * 0.5 + 1
+            li = torch.randn(DI, DS, 3, generator=g, device="cuda") * 0.1
+            Dv = torch.ones(DI, device="cuda")
+            fn = lambda: K.ssm_forward_fused_dl(delta, s, Bq, Cq, la, li, Dv)
+            nbytes = ssm_bytes(B, T, DI, DS)
+        elif args.mode in ("cumprod", "cayley"):
+            q = torch.randn(2, 256, 768, 64, 4, generator=g, device="cuda")
+            q = q / q.norm(dim=-1, keepdim=True)
+            fn = ((lambda: K.parallel_scan_quaternion(q)) if args.mode == "cumprod"
+                  else (lambda: K.cayley_discretization_fused(q)))
+            nbytes = 2 * q.numel() * 4
+        elif args.mode == "qln":
+            y = torch.randn(B, T, DI, 4, generator=g, device="cuda").to(torch.bfloat16)
+            gm = torch.ones(DI, device="cuda")
+            bt = torch.zeros(DI, 4, device="cuda")
+            fn = lambda: K.quaternion_layer_norm_fused(y, gm, bt)
+            nbytes = qln_bytes(B * T, DI)
+        elif args.mode == "copy":
+            src = torch.empty(1 << 28, device="cuda")  # 1 GiB
+            dst = torch.empty_like(src)
+            fn = lambda: dst.copy_(src)
+            nbytes = 2 * src.numel() * 4
+        else:
+            raise SystemExit(f"unknown mode {args.mode}")
+        for _ in range(args.warmup):
+            fn()
+        ms = event_time_ms(fn, reps)
+    print(json.dumps({"mode": args.mode, "mean_ms": round(ms, 4), "bytes": nbytes,
+                      "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--mode", default="full")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build's hot path runs on a single MI355X "
+              "(multi-GPU sharding is a design note, not implemented); use --gpus 1",
+              file=sys.stderr)
+        raise SystemExit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a ROCm GPU")
+    if args.mode == "full":
+        run_full(args)
+    else:
+        run_kernel_loop(args)
+
+
+if __name__ == "__main__":
+    main()

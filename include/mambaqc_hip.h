@@ -1,0 +1,136 @@
+/*
+ * mambaqc_hip.h — C ABI of libmambaqc_hip.so, the MI355X (gfx950) kernels of
+ * the Quaternion Mamba-2 SSM hot path.
+ *
+ * Conventions shared by every entry point
+ *   - All tensor arguments are device pointers to contiguous, row-major
+ *     buffers owned by the caller. Nothing is allocated inside the library.
+ *   - A quaternion is four consecutive elements (w, x, y, z).
+ *   - `dtype` selects the storage type of the tensors named in each comment:
+ *     MQC_F32, MQC_BF16 or MQC_F16. Arithmetic is always fp32. Parameter
+ *     arrays typed `const float*` are fp32 whatever `dtype` is.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream). Every call
+ *     only enqueues work; it never synchronises.
+ *   - The return value is MQC_OK (0), a negative MQC_E_* code when argument
+ *     validation fails (checked before any HIP call, so these are safe to
+ *     probe without a GPU), or a positive hipError_t from the launch.
+ *   - No global mutable state: calls are re-entrant and thread-safe.
+ *
+ * Each function names the reference interface (polux06/mambaqc) it replaces.
+ */
+#ifndef MAMBAQC_HIP_H
+#define MAMBAQC_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MQC_F32 0
+#define MQC_BF16 1
+#define MQC_F16 2
+
+#define MQC_OK 0
+#define MQC_E_NULL (-1)      /* a required pointer is NULL */
+#define MQC_E_SHAPE (-2)     /* a size is negative or inconsistent */
+#define MQC_E_DTYPE (-3)     /* unknown dtype code */
+#define MQC_E_ALIGN (-4)     /* a pointer is not aligned for the vector loads */
+#define MQC_E_LIMIT (-5)     /* a size is beyond what the kernels support */
+
+/* Human-readable text for a status code (static storage, never NULL). */
+const char* mqc_status_string(int status);
+
+/* ABI version: bumped whenever a signature changes. */
+int mqc_abi_version(void);
+
+/* out = p (x) q, Hamilton product of n_quat quaternions. p, q, out: dtype.
+ * Replaces quaternion_multiply, mambaqc/kernels/quaternion_ops.py:259-303
+ * (and quaternion_multiply_batched, :306-357, which computes the same thing). */
+int mqc_quaternion_multiply(const void* p, const void* q, void* out, int64_t n_quat,
+                            int dtype, void* stream);
+
+/* out = conj(q). Replaces quaternion_conjugate, quaternion_ops.py:360-391. */
+int mqc_quaternion_conjugate(const void* q, void* out, int64_t n_quat, int dtype, void* stream);
+
+/* out = conj(q) / max(|q|^2, eps). Replaces quaternion_inverse, quaternion_ops.py:394-428. */
+int mqc_quaternion_inverse(const void* q, void* out, int64_t n_quat, float eps, int dtype,
+                           void* stream);
+
+/* out[i] = |q_i| (n_quat scalars). Replaces quaternion_norm, quaternion_ops.py:431-461. */
+int mqc_quaternion_norm(const void* q, void* out, int64_t n_quat, int dtype, void* stream);
+
+/* q = (1 - z/2)^-1 (x) (1 + z/2) per quaternion, the inverse taken as
+ * conj/max(|.|^2, eps). z, q: dtype, n_quat quaternions.
+ * Replaces cayley_discretization_fused, mambaqc/kernels/cayley_transform.py:132-195. */
+int mqc_cayley_fwd(const void* z, void* q, int64_t n_quat, float eps, int dtype, void* stream);
+
+/* Inclusive left-ordered cumulative Hamilton product along the seq axis:
+ *   out[b,t,l] = q[b,t,l] (x) out[b,t-1,l],  out[b,-1,l] = 1.
+ * q, out: dtype, shape [batch, seq_len, lanes, 4]; lanes = d_model * d_state
+ * for the reference's [B,T,D,S,4] layout.
+ * Replaces parallel_scan_quaternion, mambaqc/kernels/parallel_scan.py:171-264,
+ * with the semantics of parallel_scan_quaternion_reference, :267-295. */
+int mqc_cumprod_scan_fwd(const void* q, void* out, int64_t batch, int64_t seq_len,
+                         int64_t lanes, int dtype, void* stream);
+
+/* Quaternion SSM over a materialised evolution operator q:
+ *   h_t = q_t (x) h_{t-1} + B_t (x) S_t      (S broadcast over d_state)
+ *   y_t = sum_k C_{t,k} (x) h_{t,k} + D_t * S_t
+ * q, B, C: dtype [batch, seq_len, d_inner, d_state, 4]; S: dtype
+ * [batch, seq_len, d_inner, 4]; D: dtype, element (b,t,d) at
+ * D[b*d_sb + t*d_st + d*d_sd] (strides in elements, 0 allowed, so an expanded
+ * [d_inner] vector needs no copy); h0: dtype [batch, d_inner, d_state, 4] or
+ * NULL for zeros; y: dtype [batch, seq_len, d_inner, 4]; h_last: dtype
+ * [batch, d_inner, d_state, 4] or NULL.
+ * Replaces ssm_forward_fused, mambaqc/kernels/ssm_fused.py:340-401, and (with
+ * seq_len = 1, h0 = h_prev, h_last = h_new) ssm_step_fused, :258-337. */
+int mqc_ssm_q_fwd(const void* q, const void* B, const void* S, const void* C, const void* D,
+                  int64_t d_sb, int64_t d_st, int64_t d_sd, const void* h0, void* y,
+                  void* h_last, int64_t batch, int64_t seq_len, int64_t d_inner,
+                  int64_t d_state, int dtype, void* stream);
+
+/* The block's fused SSM: Cayley discretisation of z = delta * Lambda computed
+ * in registers, the recurrence above with S = (s, 0, 0, 0), and the k-reduction.
+ *   Lambda[d,k] = (-softplus(lambda_alpha[d,k]), tanh(lambda_imag[d,k,0:3]))
+ *   q_t = Cayley(delta[b,t,d] * Lambda[d,k]) with eps
+ *   h_t = q_t (x) h_{t-1} + s[b,t,d] * B_t
+ *   y_t = sum_k C_{t,k} (x) h_{t,k} + (D[d] * s[b,t,d], 0, 0, 0)
+ * delta, s: dtype [batch, seq_len, d_inner]; B, C: dtype
+ * [batch, seq_len, d_inner, d_state, 4]; lambda_alpha: fp32 [d_inner, d_state];
+ * lambda_imag: fp32 [d_inner, d_state, 3]; D: fp32 [d_inner]; h0: dtype
+ * [batch, d_inner, d_state, 4] or NULL; y: dtype [batch, seq_len, d_inner, 4];
+ * h_last: dtype [batch, d_inner, d_state, 4] or NULL.
+ * Replaces the body of QuaternionMamba2Block._ssm_forward,
+ * mambaqc/models/quaternion_mamba2_block.py:206-228 (Lambda, z = delta*Lambda,
+ * cayley_discretization_fused, ssm_forward_fused), without materialising z or q. */
+int mqc_ssm_fused_fwd(const void* delta, const void* s, const void* B, const void* C,
+                      const float* lambda_alpha, const float* lambda_imag, const float* D,
+                      const void* h0, void* y, void* h_last, int64_t batch, int64_t seq_len,
+                      int64_t d_inner, int64_t d_state, float eps, int dtype, void* stream);
+
+/* Quaternion LayerNorm over the d axis of each of `rows` rows of d quaternions:
+ *   n = sqrt(|q|^2 + eps); mu, var = mean and biased variance of n over d;
+ *   out = gamma * (n - mu) / sqrt(var + eps) * q / (n + eps) + beta.
+ * q, out: dtype [rows, d, 4]; gamma: fp32 [d]; beta: fp32 [d, 4];
+ * mean, rstd: fp32 [rows] or NULL (saved statistics).
+ * Replaces quaternion_layer_norm_fused / QuaternionLayerNorm.forward,
+ * mambaqc/kernels/quaternion_norm.py:119-215, with the semantics of
+ * quaternion_layer_norm_reference, :219-245. */
+int mqc_qln_fwd(const void* q, const float* gamma, const float* beta, void* out, float* mean,
+                float* rstd, int64_t rows, int64_t d, float eps, int dtype, void* stream);
+
+/* Output step epilogue of the block: out = x + sigmoid(z) * y_real, where
+ * x, y_real, out: dtype [rows, cols] contiguous and z: dtype with element
+ * (r, c) at z[r * z_row_stride + c] (the gate half of in_proj's output).
+ * Replaces mambaqc/models/quaternion_mamba2_block.py:159-164 (gating + residual),
+ * with the gate sliced to the first d_model features as in
+ * mambaqc/models/quaternion_mamba2_lite_block.py:163. */
+int mqc_out_gate_fwd(const void* x, const void* z, int64_t z_row_stride, const void* y_real,
+                     void* out, int64_t rows, int64_t cols, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBAQC_HIP_H */

@@ -1,0 +1,131 @@
+"""ctypes binding of libmambaqc_hip.so (declared in include/mambaqc_hip.h).
+
+The library is the only compute path of this package: there is no CPU or
+torch fallback. Loading fails loudly with the build command if the library is
+absent, and every entry point checks that its tensors live on a ROCm device.
+
+torch is imported before the library is opened so that the HIP runtime torch
+ships (soname libamdhip64.so.7) is the one the library binds to; streams and
+device pointers handed across are then valid on both sides.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmambaqc_hip.so"
+
+F32, BF16, F16 = 0, 1, 2
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+
+# name -> argtypes (all return int status)
+SIGNATURES = {
+    "mqc_quaternion_multiply": [_vp, _vp, _vp, _i64, _int, _vp],
+    "mqc_quaternion_conjugate": [_vp, _vp, _i64, _int, _vp],
+    "mqc_quaternion_inverse": [_vp, _vp, _i64, _f32, _int, _vp],
+    "mqc_quaternion_norm": [_vp, _vp, _i64, _int, _vp],
+    "mqc_cayley_fwd": [_vp, _vp, _i64, _f32, _int, _vp],
+    "mqc_cumprod_scan_fwd": [_vp, _vp, _i64, _i64, _i64, _int, _vp],
+    "mqc_ssm_q_fwd": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp,
+                      _i64, _i64, _i64, _i64, _int, _vp],
+    "mqc_ssm_fused_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                          _i64, _i64, _i64, _i64, _f32, _int, _vp],
+    "mqc_qln_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _int, _vp],
+    "mqc_out_gate_fwd": [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _int, _vp],
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
+    """Open the library once per process and declare every entry point."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise NativeLibraryMissing(
+                f"{p} is missing: build it with `python -m mambaqc_amd.build` "
+                "(mambaqc_amd has no CPU fallback)")
+        lib = ctypes.CDLL(str(p))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = _int
+        lib.mqc_status_string.argtypes = [_int]
+        lib.mqc_status_string.restype = ctypes.c_char_p
+        lib.mqc_abi_version.argtypes = []
+        lib.mqc_abi_version.restype = _int
+        if lib.mqc_abi_version() != 1:
+            raise NativeLibraryMissing(f"{p}: ABI version {lib.mqc_abi_version()} != 1; rebuild")
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def status_string(status: int) -> str:
+    return load().mqc_status_string(status).decode()
+
+
+def check(status: int, name: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{name} failed with status {status}: {status_string(status)}")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected float32, bfloat16 or float16") from None
+
+
+def require_device(name: str, *tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(
+                f"mambaqc_amd.{name}: expected tensors on a ROCm device, got {t.device}; "
+                "this package runs only on the GPU")
+    dev = tensors[0].device
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"mambaqc_amd.{name}: tensors on different devices ({dev}, {t.device})")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def aligned16(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous and 16-byte aligned (the kernels' vector width)."""
+    t = t.contiguous()
+    if t.data_ptr() % 16 != 0:
+        t = t.clone()
+    return t
+
+
+def call(name: str, device_tensor: torch.Tensor, *args) -> None:
+    lib = load()
+    with torch.cuda.device(device_tensor.device):
+        status = getattr(lib, name)(*args)
+    check(status, name)

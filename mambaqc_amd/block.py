@@ -1,0 +1,124 @@
+"""QuaternionMamba2Block on MI355X.
+
+Drop-in for mambaqc/models/quaternion_mamba2_block.py:37-237: same constructor
+signature, the same parameters created in the same order (identical weights
+under the same seed, identical state_dict keys), and the same forward:
+
+    xz = in_proj(x); x_in, z = chunk(xz)                    torch GEMM
+    x_act = silu(conv1d(x_in))                              torch
+    delta = softplus(dt_proj(x_act)); s = sigmoid(gate_proj(x_act)) * x_act
+    B, C = B_proj(x_act), C_proj(x_act) as [B,T,D,S,4]      torch GEMMs (hipBLASLt)
+    y = SSM(Cayley(delta * Lambda), B, s, C, D)             HIP: ssm_forward_fused_dl
+    y = QuaternionLayerNorm(y)                              HIP: mqc_qln_fwd
+    y_real = out_proj(y)                                    torch GEMM
+    out = x + sigmoid(z[..., :d_model]) * y_real            HIP: mqc_out_gate_fwd
+
+z, q and the quaternion S are never materialised: the SSM kernel discretises
+in registers and takes the real selected signal s.
+
+The gate uses z[..., :d_model]. The reference multiplies sigmoid(z), which has
+d_inner = expand_factor * d_model features, by y_real, which has d_model
+(block.py:157-161); that broadcast fails for any expand_factor != 1. The
+reference's own Lite block gates with z[..., :d_model]
+(quaternion_mamba2_lite_block.py:163), which is the rule used here. It is
+identical to the reference whenever expand_factor == 1.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _native as nat
+from .kernels.quaternion_norm import QuaternionLayerNorm
+from .kernels.ssm_fused import ssm_forward_fused_dl
+from .layers.causal_conv1d import CausalConv1d
+from .layers.quaternion_linear import quaternion_to_real_projection, real_to_quaternion_projection
+
+
+def out_gate(x: torch.Tensor, z: torch.Tensor, y_real: torch.Tensor) -> torch.Tensor:
+    """x + sigmoid(z[..., :d]) * y_real for x, y_real [..., d] and z [..., >= d].
+
+    z may be a strided view whose last axis is contiguous (the gate half of
+    in_proj's output); it is read in place.
+    """
+    d = x.shape[-1]
+    assert y_real.shape == x.shape, f"y_real {tuple(y_real.shape)} vs x {tuple(x.shape)}"
+    assert z.shape[:-1] == x.shape[:-1] and z.shape[-1] >= d
+    nat.require_device("out_gate", x, z, y_real)
+    dtype = y_real.dtype
+    x = nat.aligned16(x.to(dtype))
+    z = z.to(dtype)
+    if z.stride(-1) != 1 or (z.dim() > 1 and not _rows_uniform(z)):
+        z = z[..., :d].contiguous()
+    y_real = nat.aligned16(y_real)
+    rows = x.numel() // d if d else 0
+    zs = z.stride(-2) if z.dim() > 1 else z.shape[-1]
+    out = torch.empty_like(x)
+    nat.call("mqc_out_gate_fwd", x, x.data_ptr(), z.data_ptr(), zs, y_real.data_ptr(),
+             out.data_ptr(), rows, d, nat.dtype_code(x), nat.stream_of(x))
+    return out
+
+
+def _rows_uniform(z: torch.Tensor) -> bool:
+    """True when all leading axes of z collapse to a single row stride."""
+    expected = z.stride(-2)
+    for i in range(z.dim() - 2, 0, -1):
+        expected *= z.shape[i]
+        if z.shape[i - 1] > 1 and z.stride(i - 1) != expected:
+            return False
+    return True
+
+
+class QuaternionMamba2Block(nn.Module):
+    """One Quaternion Mamba-2 block. Input and output: [batch, seq_len, d_model]."""
+
+    def __init__(self, d_model: int, d_state: int = 64, d_conv: int = 4,
+                 expand_factor: int = 2, dt_rank: str | int = "auto", bias: bool = False):
+        super().__init__()
+        self.d_model = d_model
+        self.d_state = d_state
+        self.d_conv = d_conv
+        self.d_inner = d_model * expand_factor
+        self.dt_rank = max(16, d_model // 16) if dt_rank == "auto" else dt_rank
+        D = self.d_inner
+
+        # Parameter creation order fixes the RNG stream (block.py:78-122).
+        self.in_proj = nn.Linear(d_model, 2 * D, bias=bias)
+        self.conv1d = CausalConv1d(D, kernel_size=d_conv, bias=True)
+        self.Lambda_alpha = nn.Parameter(torch.randn(D, d_state) * 0.5 + 1.0)
+        self.Lambda_imag = nn.Parameter(torch.randn(D, d_state, 3) * 0.1)
+        self.dt_proj = nn.Linear(D, D, bias=True)
+        self.B_proj = real_to_quaternion_projection(D, D * d_state, bias=False)
+        self.C_proj = real_to_quaternion_projection(D, D * d_state, bias=False)
+        self.D = nn.Parameter(torch.ones(D))
+        self.gate_proj = nn.Linear(D, D, bias=False)
+        self.norm = QuaternionLayerNorm(D, eps=1e-5)
+        self.out_proj = quaternion_to_real_projection(D, d_model, bias=bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            raise NotImplementedError(
+                "QuaternionMamba2Block (mambaqc_amd) has no backward yet; run the forward under "
+                "torch.no_grad() or torch.inference_mode()")
+        xz = self.in_proj(x)
+        x_in, z = xz.chunk(2, dim=-1)
+        x_act = F.silu(self.conv1d(x_in))
+        y = self._ssm_forward(x_act)
+        y = self.norm(y)
+        y_real = self.out_proj(y)
+        return out_gate(x, z, y_real)
+
+    def _ssm_forward(self, x: torch.Tensor) -> torch.Tensor:
+        """x: [batch, seq_len, d_inner] (real) -> y: [batch, seq_len, d_inner, 4]."""
+        b, t, D = x.shape
+        delta = F.softplus(self.dt_proj(x))
+        Bq = self.B_proj(x).view(b, t, D, self.d_state, 4)
+        Cq = self.C_proj(x).view(b, t, D, self.d_state, 4)
+        s = torch.sigmoid(self.gate_proj(x)) * x
+        return ssm_forward_fused_dl(delta, s, Bq, Cq, self.Lambda_alpha, self.Lambda_imag,
+                                    self.D, eps=1e-6)
+
+    def extra_repr(self) -> str:
+        return (f"d_model={self.d_model}, d_state={self.d_state}, d_inner={self.d_inner}, "
+                f"d_conv={self.d_conv}, dt_rank={self.dt_rank}")

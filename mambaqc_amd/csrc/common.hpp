@@ -1,0 +1,185 @@
+// Shared device helpers for the mambaqc_amd HIP kernels (gfx950 / CDNA4).
+//
+// Storage dtypes: fp32, bf16, fp16. All arithmetic is fp32. A quaternion is
+// four consecutive elements (w, x, y, z) of the innermost axis, exactly as in
+// the reference's [..., 4] tensors (mambaqc/kernels/quaternion_ops.py:259-282).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mambaqc_hip.h"
+
+namespace mqc {
+
+// ---------------------------------------------------------------------------
+// Storage types. bf16 and fp16 are carried as raw 16-bit patterns so that the
+// loads below can fetch several of them with one 8- or 16-byte instruction.
+// ---------------------------------------------------------------------------
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+template <typename T> struct io;
+
+template <> struct io<float> {
+  static constexpr int bytes = 4;
+  __device__ static inline float to_f32(float v) { return v; }
+  __device__ static inline float from_f32(float v) { return v; }
+};
+
+template <> struct io<bf16_t> {
+  static constexpr int bytes = 2;
+  __device__ static inline float bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+  __device__ static inline float to_f32(bf16_t v) { return bits_to_f32(v.bits); }
+  // Round to nearest even, NaN kept quiet: the same rounding torch uses for
+  // float -> bfloat16 conversions.
+  __device__ static inline bf16_t from_f32(float f) {
+    uint32_t u = __float_as_uint(f);
+    bf16_t r;
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+      r.bits = 0x7fc0u;
+    } else {
+      u += 0x7fffu + ((u >> 16) & 1u);
+      r.bits = (uint16_t)(u >> 16);
+    }
+    return r;
+  }
+};
+
+template <> struct io<f16_t> {
+  static constexpr int bytes = 2;
+  __device__ static inline float bits_to_f32(uint32_t b) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)b);
+    return (float)h;
+  }
+  __device__ static inline float to_f32(f16_t v) { return bits_to_f32(v.bits); }
+  __device__ static inline f16_t from_f32(float f) {
+    _Float16 h = (_Float16)f;
+    f16_t r;
+    r.bits = __builtin_bit_cast(uint16_t, h);
+    return r;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Vector loads of N consecutive elements (N*bytes is 8 or a multiple of 16)
+// into fp32 registers. The pointer must be aligned to min(16, N*bytes).
+// ---------------------------------------------------------------------------
+template <typename T, int N>
+__device__ inline void load_vec(const T* __restrict__ p, float (&out)[N]) {
+  if constexpr (sizeof(T) == 4) {
+    static_assert(N % 4 == 0, "fp32 loads come in float4 units");
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      float4 v = reinterpret_cast<const float4*>(p)[i];
+      out[4 * i + 0] = v.x;
+      out[4 * i + 1] = v.y;
+      out[4 * i + 2] = v.z;
+      out[4 * i + 3] = v.w;
+    }
+  } else {
+    if constexpr (N % 8 == 0) {
+#pragma unroll
+      for (int i = 0; i < N / 8; ++i) {
+        uint4 v = reinterpret_cast<const uint4*>(p)[i];
+        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          out[8 * i + 2 * c + 0] = io<T>::bits_to_f32(w[c] & 0xffffu);
+          out[8 * i + 2 * c + 1] = io<T>::bits_to_f32(w[c] >> 16);
+        }
+      }
+    } else {
+      static_assert(N == 4, "16-bit loads come in 4- or 8-element units");
+      uint2 v = *reinterpret_cast<const uint2*>(p);
+      out[0] = io<T>::bits_to_f32(v.x & 0xffffu);
+      out[1] = io<T>::bits_to_f32(v.x >> 16);
+      out[2] = io<T>::bits_to_f32(v.y & 0xffffu);
+      out[3] = io<T>::bits_to_f32(v.y >> 16);
+    }
+  }
+}
+
+// bf16 specialisation of the unpack: the high half needs only a mask, the low
+// half a shift (one VALU op per element instead of two).
+template <>
+__device__ inline void load_vec<bf16_t, 8>(const bf16_t* __restrict__ p, float (&out)[8]) {
+  uint4 v = *reinterpret_cast<const uint4*>(p);
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    out[2 * c + 0] = __uint_as_float(w[c] << 16);
+    out[2 * c + 1] = __uint_as_float(w[c] & 0xffff0000u);
+  }
+}
+
+template <typename T, int N>
+__device__ inline void store_vec(T* __restrict__ p, const float (&in)[N]) {
+  if constexpr (sizeof(T) == 4) {
+    static_assert(N % 4 == 0, "fp32 stores come in float4 units");
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      float4 v;
+      v.x = in[4 * i + 0];
+      v.y = in[4 * i + 1];
+      v.z = in[4 * i + 2];
+      v.w = in[4 * i + 3];
+      reinterpret_cast<float4*>(p)[i] = v;
+    }
+  } else {
+    static_assert(N % 4 == 0, "16-bit stores come in 4-element units");
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      uint32_t lo = io<T>::from_f32(in[4 * i + 0]).bits | ((uint32_t)io<T>::from_f32(in[4 * i + 1]).bits << 16);
+      uint32_t hi = io<T>::from_f32(in[4 * i + 2]).bits | ((uint32_t)io<T>::from_f32(in[4 * i + 3]).bits << 16);
+      reinterpret_cast<uint2*>(p)[i] = make_uint2(lo, hi);
+    }
+  }
+}
+
+template <typename T>
+__device__ inline float load_scalar(const T* __restrict__ p) {
+  return io<T>::to_f32(*p);
+}
+
+template <typename T>
+__device__ inline void store_scalar(T* __restrict__ p, float v) {
+  *p = io<T>::from_f32(v);
+}
+
+// ---------------------------------------------------------------------------
+// Hamilton product r = p (x) q (textbook form; reference
+// mambaqc/kernels/quaternion_ops.py:278-281).
+// ---------------------------------------------------------------------------
+struct quat { float w, x, y, z; };
+
+__device__ inline quat qmul(const quat& p, const quat& q) {
+  quat r;
+  r.w = p.w * q.w - p.x * q.x - p.y * q.y - p.z * q.z;
+  r.x = p.w * q.x + p.x * q.w + p.y * q.z - p.z * q.y;
+  r.y = p.w * q.y - p.x * q.z + p.y * q.w + p.z * q.x;
+  r.z = p.w * q.z + p.x * q.y - p.y * q.x + p.z * q.w;
+  return r;
+}
+
+// acc += p (x) q
+__device__ inline void qmul_acc(quat& acc, const quat& p, const quat& q) {
+  acc.w = fmaf(p.w, q.w, fmaf(-p.x, q.x, fmaf(-p.y, q.y, fmaf(-p.z, q.z, acc.w))));
+  acc.x = fmaf(p.w, q.x, fmaf(p.x, q.w, fmaf(p.y, q.z, fmaf(-p.z, q.y, acc.x))));
+  acc.y = fmaf(p.w, q.y, fmaf(-p.x, q.z, fmaf(p.y, q.w, fmaf(p.z, q.x, acc.y))));
+  acc.z = fmaf(p.w, q.z, fmaf(p.x, q.y, fmaf(-p.y, q.x, fmaf(p.z, q.w, acc.z))));
+}
+
+__device__ inline quat quat_from(const float* v) { return quat{v[0], v[1], v[2], v[3]}; }
+
+// ---------------------------------------------------------------------------
+// Launch helpers
+// ---------------------------------------------------------------------------
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MQC_OK : (int)e;
+}
+
+inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+}  // namespace mqc

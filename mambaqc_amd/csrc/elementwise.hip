@@ -1,0 +1,302 @@
+// Element-wise quaternion kernels: Hamilton product, conjugate, inverse, norm,
+// Cayley discretisation, and the block's gate + residual epilogue.
+//
+// All of these are HBM-bound streams: each thread moves 16 bytes per operand
+// per item (one float4 or eight 16-bit values) and keeps ITEMS independent
+// items in flight so a wave has several loads outstanding.
+#include "common.hpp"
+
+namespace mqc {
+
+constexpr int kThreads = 256;
+constexpr int kItems = 4;  // independent items per thread per loop trip
+
+// Quaternions per 16-byte vector for a storage type.
+template <typename T> constexpr int qpv() { return 16 / (4 * (int)sizeof(T)); }
+
+inline int64_t grid_for(int64_t units, int64_t per_block) {
+  int64_t g = (units + per_block - 1) / per_block;
+  // Large enough to fill 256 CUs many times over; items are spread by a
+  // grid-stride loop beyond that.
+  const int64_t cap = 256 * 64;
+  return g < 1 ? 1 : (g > cap ? cap : g);
+}
+
+// ---------------------------------------------------------------------------
+// Generic unary / binary map over n quaternions. QV quaternions per vector
+// access; n_vec full vectors, then a scalar (one-quaternion) tail.
+// ---------------------------------------------------------------------------
+template <typename T, int QV, typename Op>
+__global__ __launch_bounds__(kThreads) void map_kernel(const T* __restrict__ a,
+                                                       const T* __restrict__ b,
+                                                       T* __restrict__ out, int64_t n_quat,
+                                                       Op op) {
+  constexpr int E = 4 * QV;
+  const int64_t n_vec = n_quat / QV;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  for (; i + (kItems - 1) * stride < n_vec; i += kItems * stride) {
+    float va[kItems][E], vb[kItems][E];
+#pragma unroll
+    for (int u = 0; u < kItems; ++u) {
+      load_vec<T, E>(a + (i + u * stride) * E, va[u]);
+      if (b) load_vec<T, E>(b + (i + u * stride) * E, vb[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kItems; ++u) {
+      float vo[E];
+#pragma unroll
+      for (int qd = 0; qd < QV; ++qd) op(&va[u][4 * qd], b ? &vb[u][4 * qd] : nullptr, &vo[4 * qd]);
+      store_vec<T, E>(out + (i + u * stride) * E, vo);
+    }
+  }
+  for (; i < n_vec; i += stride) {
+    float va[E], vb[E], vo[E];
+    load_vec<T, E>(a + i * E, va);
+    if (b) load_vec<T, E>(b + i * E, vb);
+#pragma unroll
+    for (int qd = 0; qd < QV; ++qd) op(&va[4 * qd], b ? &vb[4 * qd] : nullptr, &vo[4 * qd]);
+    store_vec<T, E>(out + i * E, vo);
+  }
+  // Tail quaternions that do not fill a vector (only when QV > 1).
+  if (QV > 1 && blockIdx.x == 0) {
+    int64_t t = n_vec * QV + threadIdx.x;
+    if (t < n_quat) {
+      float va[4], vb[4], vo[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        va[c] = load_scalar(a + t * 4 + c);
+        vb[c] = b ? load_scalar(b + t * 4 + c) : 0.f;
+      }
+      op(va, b ? vb : nullptr, vo);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) store_scalar(out + t * 4 + c, vo[c]);
+    }
+  }
+}
+
+struct OpMul {
+  __device__ void operator()(const float* p, const float* q, float* r) const {
+    quat o = qmul(quat_from(p), quat_from(q));
+    r[0] = o.w; r[1] = o.x; r[2] = o.y; r[3] = o.z;
+  }
+};
+
+struct OpConj {
+  __device__ void operator()(const float* q, const float*, float* r) const {
+    r[0] = q[0]; r[1] = -q[1]; r[2] = -q[2]; r[3] = -q[3];
+  }
+};
+
+// conj(q) / max(|q|^2, eps)   (reference fallback quaternion_ops.py:407-410)
+struct OpInv {
+  float eps;
+  __device__ void operator()(const float* q, const float*, float* r) const {
+    float n2 = q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3];
+    n2 = fmaxf(n2, eps);
+    r[0] = q[0] / n2; r[1] = -q[1] / n2; r[2] = -q[2] / n2; r[3] = -q[3] / n2;
+  }
+};
+
+// Cayley: q = den^-1 (x) num with den = 1 - z/2, num = 1 + z/2 and
+// den^-1 = conj(den) / max(|den|^2, eps) (cayley_transform.py:199-223).
+// conj(den) and num share the axis of z's vector part, so the product
+// collapses to the closed form  q = (1 - |z|^2/4, v) / max(|den|^2, eps).
+struct OpCayley {
+  float eps;
+  __device__ void operator()(const float* z, const float*, float* r) const {
+    const float d0 = 1.f - 0.5f * z[0];
+    const float n0 = 1.f + 0.5f * z[0];
+    const float h1 = 0.5f * z[1], h2 = 0.5f * z[2], h3 = 0.5f * z[3];
+    const float hv2 = h1 * h1 + h2 * h2 + h3 * h3;
+    const float nd = fmaxf(d0 * d0 + hv2, eps);
+    r[0] = (d0 * n0 - hv2) / nd;
+    r[1] = z[1] / nd;
+    r[2] = z[2] / nd;
+    r[3] = z[3] / nd;
+  }
+};
+
+template <typename T, typename Op>
+int launch_map(const void* a, const void* b, void* out, int64_t n, Op op, hipStream_t s) {
+  if (n == 0) return MQC_OK;
+  constexpr int QV16 = qpv<T>();
+  const bool vec_ok = aligned(a, 16) && aligned(out, 16) && (!b || aligned(b, 16));
+  if (vec_ok) {
+    const int64_t g = grid_for(n / QV16 + 1, kThreads);
+    map_kernel<T, QV16, Op><<<dim3((unsigned)g), dim3(kThreads), 0, s>>>(
+        (const T*)a, (const T*)b, (T*)out, n, op);
+  } else {
+    const uintptr_t need = 4 * sizeof(T);
+    if (!aligned(a, need) || !aligned(out, need) || (b && !aligned(b, need))) return MQC_E_ALIGN;
+    if constexpr (sizeof(T) == 4) {
+      return MQC_E_ALIGN;
+    } else {
+      const int64_t g = grid_for(n, kThreads);
+      map_kernel<T, 1, Op><<<dim3((unsigned)g), dim3(kThreads), 0, s>>>(
+          (const T*)a, (const T*)b, (T*)out, n, op);
+    }
+  }
+  return launch_status();
+}
+
+template <typename Op>
+int dispatch_map(const void* a, const void* b, void* out, int64_t n, int dtype, Op op,
+                 void* stream) {
+  if (n < 0) return MQC_E_SHAPE;
+  if (n > 0 && (!a || !out)) return MQC_E_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MQC_F32: return launch_map<float>(a, b, out, n, op, s);
+    case MQC_BF16: return launch_map<bf16_t>(a, b, out, n, op, s);
+    case MQC_F16: return launch_map<f16_t>(a, b, out, n, op, s);
+    default: return MQC_E_DTYPE;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// |q| per quaternion (one scalar out per quaternion).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kThreads) void norm_kernel(const T* __restrict__ q,
+                                                        T* __restrict__ out, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+    float v[4];
+    load_vec<T, 4>(q + i * 4, v);
+    store_scalar(out + i, sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3]));
+  }
+}
+
+template <typename T>
+int launch_norm(const void* q, void* out, int64_t n, hipStream_t s) {
+  if (n == 0) return MQC_OK;
+  if (!aligned(q, 4 * sizeof(T)) || !aligned(out, sizeof(T))) return MQC_E_ALIGN;
+  norm_kernel<T><<<dim3((unsigned)grid_for(n, kThreads)), dim3(kThreads), 0, s>>>(
+      (const T*)q, (T*)out, n);
+  return launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// out = x + sigmoid(z) * y  over [rows, cols]; z rows are z_row_stride apart.
+// ---------------------------------------------------------------------------
+template <typename T, int V>
+__global__ __launch_bounds__(kThreads) void out_gate_kernel(const T* __restrict__ x,
+                                                            const T* __restrict__ z,
+                                                            int64_t zs, const T* __restrict__ y,
+                                                            T* __restrict__ out, int64_t rows,
+                                                            int64_t cols) {
+  const int64_t per_row = cols / V;
+  const int64_t n = rows * per_row;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / per_row;
+    const int64_t c = (i - r * per_row) * V;
+    float vx[V], vz[V], vy[V], vo[V];
+    if constexpr (V == 1) {
+      vx[0] = load_scalar(x + r * cols + c);
+      vz[0] = load_scalar(z + r * zs + c);
+      vy[0] = load_scalar(y + r * cols + c);
+    } else {
+      load_vec<T, V>(x + r * cols + c, vx);
+      load_vec<T, V>(z + r * zs + c, vz);
+      load_vec<T, V>(y + r * cols + c, vy);
+    }
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const float g = 1.f / (1.f + __expf(-vz[e]));
+      vo[e] = fmaf(g, vy[e], vx[e]);
+    }
+    if constexpr (V == 1) {
+      store_scalar(out + r * cols + c, vo[0]);
+    } else {
+      store_vec<T, V>(out + r * cols + c, vo);
+    }
+  }
+}
+
+template <typename T>
+int launch_out_gate(const void* x, const void* z, int64_t zs, const void* y, void* out,
+                    int64_t rows, int64_t cols, hipStream_t s) {
+  if (rows == 0 || cols == 0) return MQC_OK;
+  constexpr int V = 16 / sizeof(T);
+  const bool vec_ok = cols % V == 0 && zs % V == 0 && aligned(x, 16) && aligned(z, 16) &&
+                      aligned(y, 16) && aligned(out, 16);
+  if (vec_ok) {
+    out_gate_kernel<T, V><<<dim3((unsigned)grid_for(rows * cols / V, kThreads)), dim3(kThreads), 0,
+                            s>>>((const T*)x, (const T*)z, zs, (const T*)y, (T*)out, rows, cols);
+  } else {
+    if (!aligned(x, sizeof(T)) || !aligned(z, sizeof(T)) || !aligned(y, sizeof(T)) ||
+        !aligned(out, sizeof(T)))
+      return MQC_E_ALIGN;
+    out_gate_kernel<T, 1><<<dim3((unsigned)grid_for(rows * cols, kThreads)), dim3(kThreads), 0,
+                            s>>>((const T*)x, (const T*)z, zs, (const T*)y, (T*)out, rows, cols);
+  }
+  return launch_status();
+}
+
+}  // namespace mqc
+
+using namespace mqc;
+
+extern "C" {
+
+const char* mqc_status_string(int status) {
+  switch (status) {
+    case MQC_OK: return "ok";
+    case MQC_E_NULL: return "a required pointer is NULL";
+    case MQC_E_SHAPE: return "a size is negative or inconsistent";
+    case MQC_E_DTYPE: return "unknown dtype code";
+    case MQC_E_ALIGN: return "a pointer is not aligned for the kernel's vector loads";
+    case MQC_E_LIMIT: return "a size is beyond what the kernels support";
+    default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
+  }
+}
+
+int mqc_abi_version(void) { return 1; }
+
+int mqc_quaternion_multiply(const void* p, const void* q, void* out, int64_t n_quat, int dtype,
+                            void* stream) {
+  if (n_quat > 0 && !q) return MQC_E_NULL;
+  return dispatch_map(p, q, out, n_quat, dtype, OpMul{}, stream);
+}
+
+int mqc_quaternion_conjugate(const void* q, void* out, int64_t n_quat, int dtype, void* stream) {
+  return dispatch_map(q, nullptr, out, n_quat, dtype, OpConj{}, stream);
+}
+
+int mqc_quaternion_inverse(const void* q, void* out, int64_t n_quat, float eps, int dtype,
+                           void* stream) {
+  return dispatch_map(q, nullptr, out, n_quat, dtype, OpInv{eps}, stream);
+}
+
+int mqc_cayley_fwd(const void* z, void* q, int64_t n_quat, float eps, int dtype, void* stream) {
+  return dispatch_map(z, nullptr, q, n_quat, dtype, OpCayley{eps}, stream);
+}
+
+int mqc_quaternion_norm(const void* q, void* out, int64_t n_quat, int dtype, void* stream) {
+  if (n_quat < 0) return MQC_E_SHAPE;
+  if (n_quat > 0 && (!q || !out)) return MQC_E_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MQC_F32: return launch_norm<float>(q, out, n_quat, s);
+    case MQC_BF16: return launch_norm<bf16_t>(q, out, n_quat, s);
+    case MQC_F16: return launch_norm<f16_t>(q, out, n_quat, s);
+    default: return MQC_E_DTYPE;
+  }
+}
+
+int mqc_out_gate_fwd(const void* x, const void* z, int64_t z_row_stride, const void* y_real,
+                     void* out, int64_t rows, int64_t cols, int dtype, void* stream) {
+  if (rows < 0 || cols < 0 || z_row_stride < cols) return MQC_E_SHAPE;
+  if (rows > 0 && cols > 0 && (!x || !z || !y_real || !out)) return MQC_E_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MQC_F32: return launch_out_gate<float>(x, z, z_row_stride, y_real, out, rows, cols, s);
+    case MQC_BF16: return launch_out_gate<bf16_t>(x, z, z_row_stride, y_real, out, rows, cols, s);
+    case MQC_F16: return launch_out_gate<f16_t>(x, z, z_row_stride, y_real, out, rows, cols, s);
+    default: return MQC_E_DTYPE;
+  }
+}
+
+}  // extern "C"

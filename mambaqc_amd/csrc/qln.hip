@@ -1,0 +1,160 @@
+// Quaternion LayerNorm (mambaqc/kernels/quaternion_norm.py:219-245):
+//   n_i   = sqrt(|q_i|^2 + eps)
+//   mu    = mean_i n_i,   var = mean_i (n_i - mu)^2      (biased)
+//   out_i = gamma_i * (n_i - mu) / sqrt(var + eps) * q_i / (n_i + eps) + beta_i
+//
+// One row of d quaternions per wavefront (WPR = 1) or per workgroup of WPR
+// wavefronts. The row is read once into registers (lane L holds quaternions
+// L, L+64*WPR, ...), the two statistics are exact two-pass reductions over
+// those registers (cross-lane butterfly, then LDS across the wavefronts of a
+// workgroup), and the row is written once: one HBM read and one write per
+// element. Masked tail lanes contribute nothing to the sums, so the
+// statistics are over exactly d norms for any d.
+#include "common.hpp"
+
+namespace mqc {
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+template <int WPR>
+__device__ inline float row_sum(float v, float* red) {
+  v = wave_sum(v);
+  if constexpr (WPR == 1) {
+    return v;
+  } else {
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < WPR; ++i) s += red[i];
+    return s;
+  }
+}
+
+// NPL: quaternions per lane (register capacity); rows of d <= NPL*64*WPR.
+template <typename T, int NPL, int WPR>
+__global__ __launch_bounds__(256) void qln_kernel(const T* __restrict__ q,
+                                                  const float* __restrict__ gamma,
+                                                  const float* __restrict__ beta,
+                                                  T* __restrict__ out, float* __restrict__ mean_out,
+                                                  float* __restrict__ rstd_out, int64_t rows,
+                                                  int64_t d, float eps) {
+  constexpr int RPB = 4 / WPR;  // rows per 256-thread block
+  __shared__ float red[RPB][WPR > 1 ? WPR : 1];
+  const int tid = threadIdx.x;
+  const int sub = tid / (64 * WPR);        // row slot inside the block
+  const int t = tid - sub * 64 * WPR;      // thread index inside the row
+  const int64_t row = (int64_t)blockIdx.x * RPB + sub;
+  const bool rvalid = row < rows;
+  constexpr int TPR = 64 * WPR;
+  const T* qr = q + (rvalid ? row : 0) * d * 4;
+
+  float v[NPL][4];
+  float n[NPL];
+#pragma unroll
+  for (int m = 0; m < NPL; ++m) {
+    const int64_t i = t + (int64_t)m * TPR;
+    if (rvalid && i < d) {
+      load_vec<T, 4>(qr + i * 4, v[m]);
+    } else {
+      v[m][0] = v[m][1] = v[m][2] = v[m][3] = 0.f;
+    }
+  }
+  float s1 = 0.f;
+#pragma unroll
+  for (int m = 0; m < NPL; ++m) {
+    const int64_t i = t + (int64_t)m * TPR;
+    n[m] = sqrtf(v[m][0] * v[m][0] + v[m][1] * v[m][1] + v[m][2] * v[m][2] + v[m][3] * v[m][3] + eps);
+    if (i < d) s1 += n[m];
+  }
+  const float inv_d = 1.f / (float)d;
+  const float mu = row_sum<WPR>(s1, red[sub]) * inv_d;
+  float s2 = 0.f;
+#pragma unroll
+  for (int m = 0; m < NPL; ++m) {
+    const int64_t i = t + (int64_t)m * TPR;
+    const float c = n[m] - mu;
+    if (i < d) s2 = fmaf(c, c, s2);
+  }
+  const float var = row_sum<WPR>(s2, red[sub]) * inv_d;
+  const float rstd = 1.f / sqrtf(var + eps);
+
+  if (rvalid) {
+    if (t == 0) {
+      if (mean_out) mean_out[row] = mu;
+      if (rstd_out) rstd_out[row] = rstd;
+    }
+    T* orow = out + row * d * 4;
+#pragma unroll
+    for (int m = 0; m < NPL; ++m) {
+      const int64_t i = t + (int64_t)m * TPR;
+      if (i < d) {
+        const float f = gamma[i] * ((n[m] - mu) * rstd) / (n[m] + eps);
+        const float4 bt = reinterpret_cast<const float4*>(beta)[i];
+        float o[4] = {fmaf(f, v[m][0], bt.x), fmaf(f, v[m][1], bt.y), fmaf(f, v[m][2], bt.z),
+                      fmaf(f, v[m][3], bt.w)};
+        store_vec<T, 4>(orow + i * 4, o);
+      }
+    }
+  }
+}
+
+template <typename T, int NPL, int WPR>
+int launch_qln_n(const void* q, const float* gamma, const float* beta, void* out, float* mean,
+                 float* rstd, int64_t rows, int64_t d, float eps, hipStream_t s) {
+  constexpr int RPB = 4 / WPR;
+  const int64_t blocks = (rows + RPB - 1) / RPB;
+  if (blocks > 0x7fffffffLL) return MQC_E_LIMIT;
+  qln_kernel<T, NPL, WPR><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+      (const T*)q, gamma, beta, (T*)out, mean, rstd, rows, d, eps);
+  return launch_status();
+}
+
+template <typename T>
+int launch_qln(const void* q, const float* gamma, const float* beta, void* out, float* mean,
+               float* rstd, int64_t rows, int64_t d, float eps, hipStream_t s) {
+  if (rows == 0) return MQC_OK;
+  if (d == 0) return MQC_E_SHAPE;
+  if (!aligned(q, 4 * sizeof(T)) || !aligned(out, 4 * sizeof(T)) || !aligned(beta, 16) ||
+      !aligned(gamma, 4))
+    return MQC_E_ALIGN;
+#define MQC_QLN(NPL, WPR)                                                   \
+  if (d <= (int64_t)(NPL) * 64 * (WPR))                                     \
+    return launch_qln_n<T, NPL, WPR>(q, gamma, beta, out, mean, rstd, rows, d, eps, s);
+  MQC_QLN(1, 1)
+  MQC_QLN(2, 1)
+  MQC_QLN(4, 1)
+  MQC_QLN(8, 1)
+  MQC_QLN(16, 1)
+  MQC_QLN(24, 1)
+  MQC_QLN(32, 1)
+  MQC_QLN(16, 4)
+  MQC_QLN(32, 4)
+#undef MQC_QLN
+  return MQC_E_LIMIT;
+}
+
+}  // namespace mqc
+
+using namespace mqc;
+
+extern "C" int mqc_qln_fwd(const void* q, const float* gamma, const float* beta, void* out,
+                           float* mean, float* rstd, int64_t rows, int64_t d, float eps,
+                           int dtype, void* stream) {
+  if (rows < 0 || d < 0) return MQC_E_SHAPE;
+  if (dtype != MQC_F32 && dtype != MQC_BF16 && dtype != MQC_F16) return MQC_E_DTYPE;
+  if (rows > 0 && (!q || !gamma || !beta || !out)) return MQC_E_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MQC_F32: return launch_qln<float>(q, gamma, beta, out, mean, rstd, rows, d, eps, s);
+    case MQC_BF16: return launch_qln<bf16_t>(q, gamma, beta, out, mean, rstd, rows, d, eps, s);
+    default: return launch_qln<f16_t>(q, gamma, beta, out, mean, rstd, rows, d, eps, s);
+  }
+}

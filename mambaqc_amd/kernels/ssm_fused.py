@@ -1,0 +1,137 @@
+"""Quaternion SSM recurrence on the GPU.
+
+Mirrors mambaqc/kernels/ssm_fused.py (ssm_step_fused :258-337,
+ssm_forward_fused :340-401):
+    h_t = q_t (x) h_{t-1} + B_t (x) S_t        (S broadcast over d_state)
+    y_t = sum_k C_{t,k} (x) h_{t,k} + D_t * S_t
+One HIP launch walks every time step (the reference launches one kernel per
+step); the state never leaves registers.
+
+`ssm_forward_fused_dl` is the block's fused form: it takes delta and the raw
+Lambda parameters instead of a materialised q, computes the Cayley
+discretisation of z = delta * Lambda in registers, and takes the real
+selected signal s (S = (s, 0, 0, 0)). It replaces
+mambaqc/models/quaternion_mamba2_block.py:206-228.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _native as nat
+
+
+def _d_strides(D: torch.Tensor, dtype: torch.dtype):
+    """Return (tensor, (sb, st, sd)) for a [B, T, D] skip tensor in `dtype`.
+
+    An expanded [D] vector (zero batch and time strides, the block's
+    D.unsqueeze(0).unsqueeze(0).expand(...)) is passed without materialising it.
+    """
+    sb, st, sd = D.stride()
+    if sb == 0 and st == 0:
+        vec = D[0, 0].to(dtype).contiguous()
+        return vec, (0, 0, 1)
+    D = D.to(dtype).contiguous()
+    return D, tuple(D.stride())
+
+
+def _launch_q(q, B, S, C, D, h0, batch, T, d_model, d_state, name, want_state):
+    dtype = q.dtype
+    for t in (B, S, C):
+        if t.dtype != dtype:
+            raise TypeError(f"{name}: dtype mismatch {dtype} vs {t.dtype}")
+    q, B, S, C = (nat.aligned16(t) for t in (q, B, S, C))
+    Dt, (sb, st, sd) = D
+    y = torch.empty(batch, T, d_model, 4, device=q.device, dtype=dtype)
+    h_last = (torch.empty(batch, d_model, d_state, 4, device=q.device, dtype=dtype)
+              if want_state else None)
+    if h0 is not None:
+        if h0.dtype != dtype:
+            raise TypeError(f"{name}: dtype mismatch {dtype} vs {h0.dtype}")
+        h0 = nat.aligned16(h0)
+    nat.call("mqc_ssm_q_fwd", q, q.data_ptr(), B.data_ptr(), S.data_ptr(), C.data_ptr(),
+             Dt.data_ptr(), sb, st, sd, nat.ptr(h0), y.data_ptr(), nat.ptr(h_last),
+             batch, T, d_model, d_state, nat.dtype_code(q), nat.stream_of(q))
+    return y, h_last
+
+
+def ssm_step_fused(q: torch.Tensor, B: torch.Tensor, S: torch.Tensor, C: torch.Tensor,
+                   D: torch.Tensor, h_prev: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """One step. q, B, C, h_prev: [batch, d_model, d_state, 4]; S: [batch, d_model, 4];
+    D: [batch, d_model]. Returns (h_new, y[batch, d_model, 4]).
+
+    Reference: ssm_fused.py:258-337 (asserts :290-294).
+    """
+    batch_size, d_model, d_state, _ = q.shape
+    assert B.shape == (batch_size, d_model, d_state, 4)
+    assert S.shape == (batch_size, d_model, 4)
+    assert C.shape == (batch_size, d_model, d_state, 4)
+    assert D.shape == (batch_size, d_model)
+    assert h_prev.shape == (batch_size, d_model, d_state, 4)
+    nat.require_device("ssm_step_fused", q, B, S, C, D, h_prev)
+    Dv = D.to(q.dtype).contiguous()
+    y, h_new = _launch_q(q, B, S, C, (Dv, (Dv.stride(0), 0, Dv.stride(1))), h_prev,
+                         batch_size, 1, d_model, d_state, "ssm_step_fused", True)
+    return h_new, y.view(batch_size, d_model, 4)
+
+
+def ssm_forward_fused(q: torch.Tensor, B: torch.Tensor, S: torch.Tensor, C: torch.Tensor,
+                      D: torch.Tensor) -> torch.Tensor:
+    """All time steps from a zero state.
+
+    q, B, C: [batch, seq_len, d_model, d_state, 4]; S: [batch, seq_len, d_model, 4];
+    D: [batch, seq_len, d_model] (may be an expanded view). Returns
+    y: [batch, seq_len, d_model, 4] in q's dtype. Reference: ssm_fused.py:340-401.
+    """
+    batch_size, seq_len, d_model, d_state, _ = q.shape
+    assert B.shape == q.shape and C.shape == q.shape, "B and C must match q's shape"
+    assert S.shape == (batch_size, seq_len, d_model, 4)
+    assert D.shape == (batch_size, seq_len, d_model)
+    nat.require_device("ssm_forward_fused", q, B, S, C, D)
+    y, _ = _launch_q(q, B, S, C, _d_strides(D, q.dtype), None, batch_size, seq_len, d_model,
+                     d_state, "ssm_forward_fused", False)
+    return y
+
+
+def ssm_forward_fused_dl(delta: torch.Tensor, s: torch.Tensor, B: torch.Tensor,
+                         C: torch.Tensor, lambda_alpha: torch.Tensor,
+                         lambda_imag: torch.Tensor, D: torch.Tensor, eps: float = 1e-6,
+                         h0: torch.Tensor | None = None, return_state: bool = False):
+    """The block's SSM with the Cayley discretisation fused in.
+
+    delta, s: [batch, seq_len, d_inner]; B, C: [batch, seq_len, d_inner, d_state, 4];
+    lambda_alpha: [d_inner, d_state]; lambda_imag: [d_inner, d_state, 3]; D: [d_inner];
+    h0: optional [batch, d_inner, d_state, 4] initial state.
+    Computes Lambda = (-softplus(lambda_alpha), tanh(lambda_imag)),
+    q_t = Cayley(delta_t * Lambda, eps), and the recurrence with S = (s, 0, 0, 0).
+    Returns y [batch, seq_len, d_inner, 4] in B's dtype (and the final state if
+    return_state).
+    """
+    batch, T, d_inner, d_state, four = B.shape
+    assert four == 4
+    assert C.shape == B.shape
+    assert delta.shape == (batch, T, d_inner) and s.shape == (batch, T, d_inner)
+    assert lambda_alpha.shape == (d_inner, d_state)
+    assert lambda_imag.shape == (d_inner, d_state, 3)
+    assert D.shape == (d_inner,)
+    nat.require_device("ssm_forward_fused_dl", delta, s, B, C, lambda_alpha, lambda_imag, D)
+    dtype = B.dtype
+    if C.dtype != dtype:
+        raise TypeError(f"ssm_forward_fused_dl: dtype mismatch {dtype} vs {C.dtype}")
+    delta = nat.aligned16(delta.to(dtype))
+    s = nat.aligned16(s.to(dtype))
+    B = nat.aligned16(B)
+    C = nat.aligned16(C)
+    la = nat.aligned16(lambda_alpha.detach().float())
+    li = nat.aligned16(lambda_imag.detach().float())
+    Dv = nat.aligned16(D.detach().float())
+    y = torch.empty(batch, T, d_inner, 4, device=B.device, dtype=dtype)
+    h_last = (torch.empty(batch, d_inner, d_state, 4, device=B.device, dtype=dtype)
+              if return_state else None)
+    if h0 is not None:
+        assert h0.shape == (batch, d_inner, d_state, 4)
+        h0 = nat.aligned16(h0.to(dtype))
+    nat.call("mqc_ssm_fused_fwd", B, delta.data_ptr(), s.data_ptr(), B.data_ptr(),
+             C.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0),
+             y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state, float(eps),
+             nat.dtype_code(B), nat.stream_of(B))
+    return (y, h_last) if return_state else y

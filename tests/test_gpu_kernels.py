@@ -1,0 +1,339 @@
+"""GPU parity: every HIP kernel of libmambaqc_hip.so against the CPU oracle on
+identical seeded inputs. fp32 within rtol 1e-4, bf16/fp16 within 2e-2 (both
+with an atol floor of rtol * max|ref|); 16-bit cases compare against the
+oracle run in fp32/fp64 on the same rounded inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import GOLDEN, assert_close, tol
+
+import mambaqc_amd
+from mambaqc_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def rnd(*shape, seed=0, dtype=torch.float32, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def up(t):
+    return t.detach().cpu().double()
+
+
+def test_native_library_is_the_compute_path():
+    p = rnd(64, 4).to(DEV)
+    K.quaternion_multiply(p, p)
+    torch.cuda.synchronize()
+    maps = open("/proc/self/maps").read()
+    assert "libmambaqc_hip.so" in maps
+
+
+# ---------------------------------------------------------------- element-wise
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [0, 1, 37, 4096 + 3])
+def test_quaternion_multiply(dtype, n):
+    p, q = rnd(n, 4, seed=1, dtype=dtype), rnd(n, 4, seed=2, dtype=dtype)
+    got = K.quaternion_multiply(p.to(DEV), q.to(DEV))
+    assert got.dtype == dtype and got.shape == p.shape
+    assert_close(got, oracle.hamilton(up(p), up(q)), tol(dtype), f"qmul {dtype} n={n}")
+
+
+def test_quaternion_multiply_table_exact():
+    e = torch.eye(4, device=DEV)
+    p = e.repeat_interleave(4, 0)
+    q = e.repeat(4, 1)
+    got = K.quaternion_multiply(p, q).cpu()
+    want = oracle.hamilton(p.cpu(), q.cpu())
+    assert torch.equal(got, want)
+
+
+def test_quaternion_multiply_batched_and_views():
+    p = rnd(2, 3, 5, 7, 4, seed=3)
+    q = rnd(2, 3, 5, 7, 4, seed=4)
+    got = K.quaternion_multiply_batched(p.to(DEV), q.to(DEV))
+    assert_close(got, oracle.hamilton(up(p), up(q)), 1e-4, "qmul batched")
+    # Non-contiguous and misaligned views are accepted.
+    big = rnd(9, 4, seed=5).to(DEV)
+    got = K.quaternion_multiply(big[1:8], big[2:9])
+    assert_close(got, oracle.hamilton(up(big[1:8]), up(big[2:9])), 1e-4, "qmul offset views")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_conjugate_inverse_norm(dtype):
+    q = rnd(3, 11, 4, seed=6, dtype=dtype)
+    qd = q.to(DEV)
+    assert_close(K.quaternion_conjugate(qd), oracle.conjugate(up(q)), tol(dtype), "conj")
+    assert_close(K.quaternion_inverse(qd), oracle.inverse(up(q)), tol(dtype), "inv")
+    assert_close(K.quaternion_norm(qd), oracle.norm(up(q)), tol(dtype), "norm")
+    tiny = torch.tensor([[1e-4, 0.0, 0.0, 0.0]], device=DEV)
+    assert_close(K.quaternion_inverse(tiny, eps=1e-6), oracle.inverse(tiny.cpu(), 1e-6), 1e-4, "inv clamp")
+
+
+# ---------------------------------------------------------------- Cayley
+def test_cayley_golden():
+    d = np.load(GOLDEN / "cayley.npz")
+    z = torch.from_numpy(d["z"])
+    got = K.cayley_discretization_fused(z.to(DEV), eps=float(d["eps"]))
+    assert_close(got, torch.from_numpy(d["q"]), 1e-4, "cayley golden")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_cayley_random(dtype):
+    z = rnd(2, 8, 16, 32, 4, seed=7, dtype=dtype)
+    z[..., 0] = -z[..., 0].abs()
+    got = K.cayley_discretization_fused(z.to(DEV))
+    assert_close(got, oracle.cayley_reference(up(z)), tol(dtype), f"cayley {dtype}")
+
+
+def test_cayley_identity_and_stability():
+    z = torch.zeros(2, 4, 8, 16, 4, device=DEV)
+    q = K.cayley_discretization_fused(z)
+    want = torch.zeros_like(q)
+    want[..., 0] = 1
+    assert torch.equal(q, want)
+    z = rnd(2, 4, 8, 16, 4, seed=8).to(DEV)
+    z[..., 0] = -z[..., 0].abs() - 0.5
+    assert (K.quaternion_norm(K.cayley_discretization_fused(z)) < 1.0 + 1e-4).all()
+
+
+# ---------------------------------------------------------------- cumulative product
+@pytest.mark.parametrize("shape", [(2, 37, 5, 7), (1, 300, 3, 64), (3, 1, 2, 3), (1, 64, 1, 1), (1, 129, 130, 1)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_cumprod(shape, dtype):
+    b, T, d, k = shape
+    # Unit-norm-ish factors keep the product's magnitude O(1) over long T.
+    q = rnd(b, T, d, k, 4, seed=sum(shape), dtype=torch.float64)
+    q = (q / q.norm(dim=-1, keepdim=True)).to(dtype)
+    got = K.parallel_scan_quaternion(q.to(DEV))
+    assert got.dtype == dtype
+    assert_close(got, oracle.cumprod_reference(up(q)), tol(dtype), f"cumprod {shape} {dtype}")
+
+
+def test_cumprod_order_and_identity():
+    i = torch.tensor([0.0, 1, 0, 0])
+    j = torch.tensor([0.0, 0, 1, 0])
+    q = torch.stack([i, j]).view(1, 2, 1, 1, 4).to(DEV)
+    out = K.parallel_scan_quaternion(q).cpu().view(2, 4)
+    assert torch.equal(out[1], torch.tensor([0.0, 0, 0, -1]))
+    ident = torch.zeros(2, 10, 8, 16, 4, device=DEV)
+    ident[..., 0] = 1
+    assert torch.equal(K.parallel_scan_quaternion(ident), ident)
+    empty = torch.zeros(2, 0, 3, 4, 4, device=DEV)
+    assert K.parallel_scan_quaternion(empty).shape == empty.shape
+
+
+def test_cumprod_config2_full_size():
+    """[2,256,768,64,4] fp32 (config 2): q = Cayley(z), then the scan. A lane
+    slice is checked against the oracle; every lane is checked through
+    |cum_t| = prod_{u<=t} |q_u| (norm multiplicativity)."""
+    g = torch.Generator(device=DEV).manual_seed(0)
+    shape = (2, 256, 768, 64)
+    n = lambda: torch.randn(*shape, generator=g, device=DEV)
+    z = torch.empty(*shape, 4, device=DEV)
+    z[..., 0] = -torch.exp(n()) * torch.nn.functional.softplus(n())
+    for c in range(1, 4):
+        z[..., c] = n() * torch.nn.functional.softplus(n())
+    q = K.cayley_discretization_fused(z)
+    cum = K.parallel_scan_quaternion(q)
+    sl = (slice(None), slice(None), slice(100, 103), slice(None))
+    assert_close(q[sl], oracle.cayley_reference(z[sl].cpu()), 1e-4, "C2 cayley slice")
+    assert_close(cum[sl], oracle.cumprod_reference(q[sl].cpu()), 1e-4, "C2 scan slice")
+    logn = torch.log(K.quaternion_norm(q).double()).cumsum(1)
+    got = torch.log(K.quaternion_norm(cum).double())
+    err = (got - logn).abs().max().item()
+    assert err < 1e-3, f"norm multiplicativity violated: max |log| error {err}"
+
+
+# ---------------------------------------------------------------- SSM (materialised q)
+def _q_inputs(b, T, d, k, seed, dtype):
+    q = rnd(b, T, d, k, 4, seed=seed, dtype=torch.float64)
+    q = 0.9 * q / q.norm(dim=-1, keepdim=True)          # stable: |q| < 1
+    Bm = rnd(b, T, d, k, 4, seed=seed + 1, scale=0.5, dtype=torch.float64)
+    C = rnd(b, T, d, k, 4, seed=seed + 2, scale=0.5, dtype=torch.float64)
+    S = rnd(b, T, d, 4, seed=seed + 3, dtype=torch.float64)
+    D = rnd(d, seed=seed + 4, dtype=torch.float64)
+    return [t.to(dtype) for t in (q, Bm, S, C)] + [D.to(dtype)]
+
+
+@pytest.mark.parametrize("k", [1, 5, 16, 48, 64, 100])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_ssm_forward_fused(k, dtype):
+    b, T, d = 2, 20, 3
+    q, Bm, S, C, D = _q_inputs(b, T, d, k, seed=k, dtype=dtype)
+    Dx = D.view(1, 1, d).expand(b, T, d)
+    got = K.ssm_forward_fused(*(t.to(DEV) for t in (q, Bm, S, C)), Dx.to(DEV))
+    assert got.dtype == dtype
+    want = oracle.ssm_forward_reference(up(q), up(Bm), up(S), up(C), up(Dx))
+    assert_close(got, want, tol(dtype), f"ssm_q k={k} {dtype}")
+
+
+def test_ssm_forward_fused_strided_D():
+    b, T, d, k = 2, 9, 4, 8
+    q, Bm, S, C, _ = _q_inputs(b, T, d, k, seed=21, dtype=torch.float32)
+    D = rnd(T, b, d, seed=22).transpose(0, 1)           # non-contiguous [b, T, d]
+    got = K.ssm_forward_fused(*(t.to(DEV) for t in (q, Bm, S, C)), D.to(DEV))
+    want = oracle.ssm_forward_reference(up(q), up(Bm), up(S), up(C), up(D))
+    assert_close(got, want, 1e-4, "ssm_q strided D")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_ssm_step_fused(dtype):
+    b, d, k = 3, 5, 16
+    q, Bm, S, C, _ = _q_inputs(b, 1, d, k, seed=31, dtype=dtype)
+    q, Bm, S, C = q[:, 0], Bm[:, 0], S[:, 0], C[:, 0]
+    D = rnd(b, d, seed=32, dtype=dtype)
+    h = rnd(b, d, k, 4, seed=33, dtype=dtype)
+    h_new, y = K.ssm_step_fused(*(t.to(DEV) for t in (q, Bm, S, C, D, h)))
+    h_ref, y_ref = oracle.ssm_step_reference(up(q), up(Bm), up(S), up(C), up(D), up(h))
+    assert_close(h_new, h_ref, tol(dtype), "step h")
+    assert_close(y, y_ref, tol(dtype), "step y")
+
+
+# ---------------------------------------------------------------- SSM (block form)
+def _dl_inputs(b, T, d, k, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g)
+    delta = torch.nn.functional.softplus(r(b, T, d) - 2).to(dtype)
+    s = r(b, T, d).to(dtype)
+    Bm = (r(b, T, d, k, 4) * 0.1).to(dtype)
+    C = (r(b, T, d, k, 4) * 0.1).to(dtype)
+    la = r(d, k) * 0.5 + 1
+    li = r(d, k, 3) * 0.1
+    D = torch.ones(d) + 0.1 * r(d)
+    return delta, s, Bm, C, la, li, D
+
+
+@pytest.mark.parametrize("shape", [(1, 64, 8, 64), (2, 33, 5, 16), (1, 17, 3, 1), (2, 10, 4, 3),
+                                   (1, 12, 2, 100), (1, 9, 130, 2)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_ssm_fused_dl(shape, dtype):
+    a = _dl_inputs(*shape, seed=sum(shape), dtype=dtype)
+    got = K.ssm_forward_fused_dl(*(t.to(DEV) for t in a))
+    want = oracle.ssm_forward_dl_reference(*(up(t) for t in a))
+    assert_close(got, want, tol(dtype), f"ssm_dl {shape} {dtype}")
+
+
+def test_ssm_fused_dl_state_carry():
+    """Running [0, T) equals running [0, t1) then [t1, T) from the carried state."""
+    a = _dl_inputs(2, 40, 6, 64, seed=41, dtype=torch.float32)
+    dev = [t.to(DEV) for t in a]
+    delta, s, Bm, C, la, li, D = dev
+    y_full, h_full = K.ssm_forward_fused_dl(*dev, return_state=True)
+    y1, h1 = K.ssm_forward_fused_dl(delta[:, :15], s[:, :15], Bm[:, :15], C[:, :15], la, li, D,
+                                    return_state=True)
+    y2, h2 = K.ssm_forward_fused_dl(delta[:, 15:], s[:, 15:], Bm[:, 15:], C[:, 15:], la, li, D,
+                                    h0=h1, return_state=True)
+    assert_close(torch.cat([y1, y2], 1), y_full, 1e-5, "carry y")
+    assert_close(h2, h_full, 1e-5, "carry h")
+    ref_y, ref_h = oracle.ssm_forward_dl_reference(*(up(t) for t in a), return_state=True)
+    assert_close(h_full, ref_h, 1e-4, "final state vs oracle")
+
+
+def test_ssm_fused_dl_config3_full_size():
+    """B4 T2048 D1536 S64 bf16 (config 3 sizes). Lanes are independent, so
+    d-slices of the full-size output are checked against the oracle on the
+    same bf16 inputs. Every lane is checked through linearity in s: with q and
+    B fixed, h and the skip term are linear in s, so y(2s) = 2 y(s)."""
+    b, T, d, k = 4, 2048, 1536, 64
+    g = torch.Generator(device=DEV).manual_seed(0)
+    bf = torch.bfloat16
+    x = torch.randn(b, T, d, generator=g, device=DEV)
+    delta = torch.nn.functional.softplus(torch.randn(b, T, d, generator=g, device=DEV) - 2).to(bf)
+    Bm = (torch.randn(b, T, d, k, 4, generator=g, device=DEV, dtype=bf) * 0.02)
+    C = (torch.randn(b, T, d, k, 4, generator=g, device=DEV, dtype=bf) * 0.02)
+    la = torch.randn(d, k, generator=g, device=DEV) * 0.5 + 1
+    li = torch.randn(d, k, 3, generator=g, device=DEV) * 0.1
+    D = torch.ones(d, device=DEV)
+    s = x.to(bf)
+    y = K.ssm_forward_fused_dl(delta, s, Bm, C, la, li, D)
+    y2 = K.ssm_forward_fused_dl(delta, (2 * s.float()).to(bf), Bm, C, la, li, D)
+    assert_close(y2.float(), 2 * y.float(), 2e-2, "linearity in s")
+    for b0, ds in ((0, slice(0, 3)), (3, slice(1533, 1536))):
+        want = oracle.ssm_forward_dl_reference(
+            up(delta[b0:b0 + 1, :, ds]), up(s[b0:b0 + 1, :, ds]), up(Bm[b0:b0 + 1, :, ds]),
+            up(C[b0:b0 + 1, :, ds]), up(la[ds]), up(li[ds]), up(D[ds]))
+        assert_close(y[b0:b0 + 1, :, ds], want, 2e-2, f"C3 slice b={b0} d={ds}")
+
+
+# ---------------------------------------------------------------- QLN
+def test_qln_golden():
+    d = np.load(GOLDEN / "qln.npz")
+    q, g, bt = (torch.from_numpy(d[k]) for k in ("q", "gamma", "beta"))
+    got = K.quaternion_layer_norm_fused(q.to(DEV), g.to(DEV), bt.to(DEV), eps=float(d["eps"]))
+    assert_close(got, torch.from_numpy(d["out"]), 1e-4, "qln golden")
+
+
+@pytest.mark.parametrize("dm", [1, 7, 64, 130, 1536, 2100, 5000])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_qln(dm, dtype):
+    q = rnd(2, 3, dm, 4, seed=dm, dtype=dtype)
+    gamma = rnd(dm, seed=dm + 1).abs() + 0.5
+    beta = rnd(dm, 4, seed=dm + 2) * 0.1
+    got, mean, rstd = K.quaternion_layer_norm_fused(q.to(DEV), gamma.to(DEV), beta.to(DEV),
+                                                    return_stats=True)
+    want = oracle.qln_reference(up(q), up(gamma), up(beta))
+    assert_close(got, want, tol(dtype), f"qln d={dm} {dtype}")
+    n = torch.sqrt((up(q) ** 2).sum(-1) + 1e-5)
+    assert_close(mean, n.mean(-1), 1e-4, "qln mean")
+    assert_close(rstd, 1 / torch.sqrt(n.var(-1, unbiased=False) + 1e-5), 1e-3, "qln rstd")
+
+
+def test_qln_module():
+    m = K.QuaternionLayerNorm(24).to(DEV)
+    q = rnd(2, 5, 24, 4, seed=51).to(DEV)
+    assert_close(m(q), oracle.qln_reference(q.cpu(), m.gamma.detach().cpu(), m.beta.detach().cpu()),
+                 1e-4, "qln module")
+
+
+# ---------------------------------------------------------------- output step
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_out_gate(dtype):
+    rows, dm, di = 37, 24, 48
+    x = rnd(rows, dm, seed=61, dtype=dtype)
+    xz = rnd(rows, 2 * di, seed=62, dtype=dtype)
+    yr = rnd(rows, dm, seed=63, dtype=dtype)
+    z = xz.to(DEV).chunk(2, dim=-1)[1]
+    got = mambaqc_amd.out_gate(x.to(DEV), z, yr.to(DEV))
+    zz = up(xz)[:, di:di + dm]
+    assert_close(got, up(x) + torch.sigmoid(zz) * up(yr), tol(dtype), f"out_gate {dtype}")
+
+
+# ---------------------------------------------------------------- block
+def test_block_golden_s1e1():
+    d = np.load(GOLDEN / "block_s1e1.npz")
+    blk = mambaqc_amd.QuaternionMamba2Block(16, d_state=1, d_conv=4, expand_factor=1)
+    blk.load_state_dict({k[2:]: torch.from_numpy(d[k]) for k in d.files if k.startswith("p:")})
+    blk = blk.to(DEV)
+    with torch.no_grad():
+        got = blk(torch.from_numpy(d["x"]).to(DEV))
+    assert_close(got, torch.from_numpy(d["out"]), 1e-4, "block golden")
+
+
+def test_block_config1_vs_oracle():
+    torch.manual_seed(0)
+    blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=16, d_conv=4, expand_factor=2)
+    x = torch.randn(1, 64, 64)
+    want = oracle.block_forward_reference(blk.state_dict(), x, d_state=16)
+    with torch.no_grad():
+        got = blk.to(DEV)(x.to(DEV))
+    assert_close(got, want, 1e-4, "block C1 fp32")
+
+
+def test_block_bf16_vs_oracle():
+    torch.manual_seed(1)
+    blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=16, d_conv=4, expand_factor=2)
+    blk = blk.to(torch.bfloat16)
+    x = torch.randn(2, 48, 64).to(torch.bfloat16)
+    sd = {k: v.float() for k, v in blk.state_dict().items()}
+    want = oracle.block_forward_reference(sd, x.float(), d_state=16)
+    with torch.no_grad():
+        got = blk.to(DEV)(x.to(DEV))
+    assert got.dtype == torch.bfloat16
+    assert_close(got, want, 2e-2, "block bf16")

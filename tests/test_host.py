@@ -1,0 +1,123 @@
+"""Host-side tests that need no GPU: the C-ABI library loads and exports every
+symbol include/mambaqc_hip.h declares, argument validation answers before any
+HIP call, the Python mirror keeps the reference's assertions and refuses CPU
+tensors, the block's parameters match the reference's seeded constructor, and
+the product package never reaches the oracle.
+"""
+import ctypes
+import hashlib
+import json
+import re
+
+import pytest
+import torch
+
+from conftest import GOLDEN, ROOT
+
+import mambaqc_amd
+from mambaqc_amd import _native as nat
+from mambaqc_amd import kernels as K
+
+HEADER = ROOT / "include" / "mambaqc_hip.h"
+FAKE = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int)\s+(mqc_\w+)\(", text, re.M)))
+
+
+def test_header_declares_the_api():
+    names = declared_symbols()
+    assert len(names) == 12, names
+    assert set(nat.SIGNATURES) <= set(names)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = nat.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.mqc_abi_version() == 1
+
+
+def test_status_strings():
+    assert nat.status_string(0) == "ok"
+    for code in (-1, -2, -3, -4, -5):
+        s = nat.status_string(code)
+        assert s and s != "unknown status"
+
+
+def test_validation_codes_without_gpu():
+    lib = nat.load()
+    # NULL pointer with work to do.
+    assert lib.mqc_quaternion_multiply(None, None, None, 10, 0, None) == -1
+    # Negative size.
+    assert lib.mqc_cayley_fwd(FAKE, FAKE, -1, 1e-6, 0, None) == -2
+    # Unknown dtype.
+    assert lib.mqc_quaternion_conjugate(FAKE, FAKE, 8, 7, None) == -3
+    assert lib.mqc_ssm_fused_fwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, None,
+                                 1, 1, 1, 1, 1e-6, 9, None) == -3
+    # Misaligned quaternion pointer.
+    assert lib.mqc_cumprod_scan_fwd(ctypes.c_void_p(4097), FAKE, 1, 1, 1, 0, None) == -4
+    # d_state beyond the supported maximum.
+    assert lib.mqc_ssm_fused_fwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, None,
+                                 1, 1, 1, 300, 1e-6, 1, None) == -5
+    assert lib.mqc_ssm_q_fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 0, 1, None, FAKE, None,
+                             1, 1, 1, 257, 0, None) == -5
+    # QLN over an empty row is undefined (mean of nothing).
+    assert lib.mqc_qln_fwd(FAKE, FAKE, FAKE, FAKE, None, None, 3, 0, 1e-5, 0, None) == -2
+    # Gate row stride shorter than the row.
+    assert lib.mqc_out_gate_fwd(FAKE, FAKE, 4, FAKE, FAKE, 2, 8, 0, None) == -2
+    # Nothing to do is not an error.
+    assert lib.mqc_quaternion_multiply(None, None, None, 0, 0, None) == 0
+    assert lib.mqc_cumprod_scan_fwd(None, None, 0, 5, 5, 0, None) == 0
+
+
+def test_wrappers_keep_reference_assertions():
+    # Shape assertions fire before the device check, as in the reference.
+    with pytest.raises(AssertionError):
+        K.quaternion_multiply(torch.zeros(3, 4), torch.zeros(2, 4))
+    with pytest.raises(AssertionError):
+        K.cayley_discretization_fused(torch.zeros(2, 3, 4))
+    with pytest.raises(AssertionError):
+        K.parallel_scan_quaternion(torch.zeros(1, 2, 3, 4, 3))
+    with pytest.raises(AssertionError):
+        K.quaternion_layer_norm_fused(torch.zeros(1, 2, 3, 4), torch.ones(4), torch.zeros(3, 4))
+    with pytest.raises(AssertionError):
+        K.ssm_step_fused(torch.zeros(1, 2, 3, 4), torch.zeros(1, 2, 3, 4), torch.zeros(1, 2, 4),
+                         torch.zeros(1, 2, 3, 4), torch.zeros(1, 3), torch.zeros(1, 2, 3, 4))
+
+
+def test_wrappers_refuse_cpu_tensors():
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        K.quaternion_multiply(torch.zeros(3, 4), torch.zeros(3, 4))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        K.cayley_discretization_fused(torch.zeros(1, 2, 3, 4, 4))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        K.QuaternionLayerNorm(3)(torch.zeros(1, 2, 3, 4))
+
+
+def test_block_refuses_grad_until_backward_exists():
+    blk = mambaqc_amd.QuaternionMamba2Block(8, d_state=2)
+    with pytest.raises(NotImplementedError):
+        blk(torch.zeros(1, 3, 8))
+
+
+def test_block_seeded_init_matches_reference():
+    info = json.loads((GOLDEN / "init_c1.json").read_text())
+    torch.manual_seed(0)
+    blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=16, d_conv=4, expand_factor=2)
+    sd = blk.state_dict()
+    assert sorted(sd) == sorted(info)
+    for k, v in sd.items():
+        a = v.detach().float().contiguous().numpy()
+        assert list(a.shape) == info[k]["shape"], k
+        assert hashlib.sha256(a.tobytes()).hexdigest() == info[k]["sha256"], k
+
+
+def test_product_never_imports_oracle():
+    pkg = ROOT / "mambaqc_amd"
+    for f in pkg.rglob("*.py"):
+        src = f.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle\b", src, re.M), f
+        assert "oracle." not in src.replace("# ", ""), f
