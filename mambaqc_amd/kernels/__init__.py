@@ -2,7 +2,15 @@
 
 Same exports as mambaqc/kernels/__init__.py:10-33, each backed by a HIP kernel
 of libmambaqc_hip.so, plus the block's fused form `ssm_forward_fused_dl`.
+
+The submodule `quaternion_norm` (the layer norm) is imported before the
+element-wise ops so that the package attribute `quaternion_norm` ends up bound
+to the |q| function, not to the submodule of the same name.
 """
+from .quaternion_norm import quaternion_layer_norm_fused, QuaternionLayerNorm
+from .cayley_transform import cayley_discretization_fused
+from .parallel_scan import parallel_scan_quaternion
+from .ssm_fused import ssm_step_fused, ssm_forward_fused, ssm_forward_fused_dl
 from .quaternion_ops import (
     quaternion_multiply,
     quaternion_multiply_batched,
@@ -10,10 +18,6 @@ from .quaternion_ops import (
     quaternion_inverse,
     quaternion_norm,
 )
-from .cayley_transform import cayley_discretization_fused
-from .parallel_scan import parallel_scan_quaternion
-from .quaternion_norm import quaternion_layer_norm_fused, QuaternionLayerNorm
-from .ssm_fused import ssm_step_fused, ssm_forward_fused, ssm_forward_fused_dl
 
 __all__ = [
     "quaternion_multiply",

@@ -145,10 +145,19 @@ def test_cumprod_config2_full_size():
     sl = (slice(None), slice(None), slice(100, 103), slice(None))
     assert_close(q[sl], oracle.cayley_reference(z[sl].cpu()), 1e-4, "C2 cayley slice")
     assert_close(cum[sl], oracle.cumprod_reference(q[sl].cpu()), 1e-4, "C2 scan slice")
-    logn = torch.log(K.quaternion_norm(q).double()).cumsum(1)
-    got = torch.log(K.quaternion_norm(cum).double())
-    err = (got - logn).abs().max().item()
+    # |q| < 1 at every step (Re z < 0), so the products decay and fall below
+    # fp32's normal range (e^-87) after ~100 steps for about half the lanes.
+    # Norms are taken in float64 (squares of fp32 values near 1e-20 would
+    # underflow in fp32); multiplicativity is checked where the exact product
+    # is a normal fp32 with margin, and decay is checked everywhere else.
+    logn = torch.log(q.double().norm(dim=-1)).cumsum(1)
+    got = torch.log(cum.double().norm(dim=-1))
+    live = logn > -80.0
+    assert live.float().mean().item() > 0.3, "too few lanes left to check"
+    err = (got[live] - logn[live]).abs().max().item()
     assert err < 1e-3, f"norm multiplicativity violated: max |log| error {err}"
+    dead = logn < -95.0
+    assert (got[dead] < -85.0).all(), "products that must have decayed did not"
 
 
 # ---------------------------------------------------------------- SSM (materialised q)

@@ -121,3 +121,13 @@ def test_product_never_imports_oracle():
         src = f.read_text()
         assert not re.search(r"^\s*(from|import)\s+oracle\b", src, re.M), f
         assert "oracle." not in src.replace("# ", ""), f
+
+
+def test_kernel_exports_are_functions():
+    # `quaternion_norm` is both a submodule name and an exported function;
+    # the export must be the function (reference kernels/__init__.py:10-33).
+    import types
+    for name in K.__all__:
+        obj = getattr(K, name)
+        assert not isinstance(obj, types.ModuleType), name
+        assert callable(obj), name
