@@ -31,17 +31,11 @@ template <> struct io<bf16_t> {
   static constexpr int bytes = 2;
   __device__ static inline float bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
   __device__ static inline float to_f32(bf16_t v) { return bits_to_f32(v.bits); }
-  // Round to nearest even, NaN kept quiet: the same rounding torch uses for
-  // float -> bfloat16 conversions.
+  // Round to nearest even (gfx950's v_cvt_pk_bf16_f32), the rounding torch
+  // uses for float -> bfloat16 conversions; NaN stays NaN.
   __device__ static inline bf16_t from_f32(float f) {
-    uint32_t u = __float_as_uint(f);
     bf16_t r;
-    if ((u & 0x7fffffffu) > 0x7f800000u) {
-      r.bits = 0x7fc0u;
-    } else {
-      u += 0x7fffu + ((u >> 16) & 1u);
-      r.bits = (uint16_t)(u >> 16);
-    }
+    r.bits = __builtin_bit_cast(uint16_t, (__bf16)f);
     return r;
   }
 };
@@ -171,6 +165,47 @@ __device__ inline void qmul_acc(quat& acc, const quat& p, const quat& q) {
 }
 
 __device__ inline quat quat_from(const float* v) { return quat{v[0], v[1], v[2], v[3]}; }
+
+// ---------------------------------------------------------------------------
+// Cross-lane data movement on the VALU (wave64, gfx950). DPP reads a
+// neighbour's register inside the consuming add (v_add_f32_dpp), and the
+// permlane swaps exchange whole 16- or 32-lane rows, so none of these goes
+// through the LDS pipeline the way ds_bpermute does.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ inline float dpp_mov(float v) {
+  // bound_ctrl set: lets the compiler fold the move into the consumer. Every
+  // pattern below reads an existing lane, so the bound control never applies.
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+// Lane i reads lane i^1 / i^2 inside its quad.
+__device__ inline float lane_xor1(float v) { return dpp_mov<0xB1>(v); }  // quad_perm [1,0,3,2]
+__device__ inline float lane_xor2(float v) { return dpp_mov<0x4E>(v); }  // quad_perm [2,3,0,1]
+// Lane i reads lane (i - 4 or 8) mod 16 inside its 16-lane row.
+__device__ inline float row_rot4(float v) { return dpp_mov<0x124>(v); }  // row_ror:4
+__device__ inline float row_rot8(float v) { return dpp_mov<0x128>(v); }  // row_ror:8
+
+// The row swaps are issued as inline assembly with both registers read-write:
+// through the builtins, this compiler reads the first result in place of the
+// second one when the two are added (v + v instead of v + partner). The
+// s_nop pairs cover the VALU-write -> permlane-read dependency and the other
+// way round.
+//
+// Sum over each pair of rows, delivered to the even row: lanes 0-15 receive
+// v(0-15) + v(16-31) and lanes 32-47 receive v(32-47) + v(48-63); the odd
+// rows receive 0.
+__device__ inline float sum_row_pair_to_even(float v) {
+  float a = v, b = 0.f;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+// Sum over the two 32-lane halves, delivered to lanes 0-31 (lanes 32-63 get 0).
+__device__ inline float sum_halves_to_low(float v) {
+  float a = v, b = 0.f;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return a + b;
+}
 
 // ---------------------------------------------------------------------------
 // Launch helpers
