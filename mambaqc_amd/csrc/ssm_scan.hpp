@@ -1,0 +1,460 @@
+#pragma once
+// Quaternion selective-state-space recurrence, fused.
+//
+//   h_t = q_t (x) h_{t-1} + B_t (x) S_t        (S broadcast over d_state)
+//   y_t = sum_k C_{t,k} (x) h_{t,k} + D_t * S_t
+//
+// (mambaqc/kernels/ssm_fused.py:363-379 and :405-430.)
+//
+// Two operand forms share one kernel:
+//   MODE_DL  the block's form: q_t = Cayley(delta_t * Lambda) is computed in
+//            registers from a per-(d,k) Lambda (closed form below), S = (s,0,0,0)
+//            so B (x) S = s * B, and D is a per-d vector. Neither z nor q is
+//            ever written to memory (quaternion_mamba2_block.py:183-228).
+//   MODE_Q   q, S (full quaternion) and D (strided [B,T,D]) given explicitly,
+//            as in ssm_forward_fused / ssm_step_fused.
+//
+// Work decomposition. Every (b, d, k) is an independent sequential recurrence
+// over t. The grid is (d-blocks, batch): blockIdx.y is the batch row, so the
+// start of every (b, t) slice is a wave-uniform scalar and each lane only
+// carries a 32-bit offset inside the slice. A group of G consecutive lanes
+// owns one (b, d); lane j of the group owns KPL consecutive k (one lane reads
+// KPL*4 contiguous elements of B and of C per step: 16 bytes for bf16 with
+// KPL = 2). Lanes past the last d or the last k are clamped onto valid
+// addresses instead of being branched around, so the per-step loads carry no
+// predicate; their results are discarded (past-d groups store nothing,
+// past-k lanes are zeroed before the k-sum).
+//
+// Each lane walks all T steps with its KPL states in registers and a ring of
+// PF steps of operands in flight (raw bits, unpacked when consumed). A slot is
+// consumed before it is refilled with step t+PF, so the ring needs no copies.
+// The waves of a block are kept on the same step by a barrier (see
+// launch_ssm_shape), which keeps each block's reads of a (b, t) slice together.
+//
+// The per-step sum over k: an FMA chain over the lane's KPL states, then a
+// G-lane transpose-reduce on the VALU. The first two butterfly stages (DPP
+// quad permutes) swap half of the four components with the partner lane
+// instead of reducing all four, so afterwards each lane carries one component
+// and the remaining stages are single adds: DPP row rotations by 4 and 8 inside
+// a 16-lane row, then permlane16/permlane32 swaps across rows.
+//
+// Cayley closed form. For z = (a, v), den = 1 - z/2, num = 1 + z/2:
+//   den^-1 (x) num = (1 - |z|^2/4, v) / max(|den|^2, eps),
+//   |den|^2 = 1 - a + |z|^2/4,
+// because conj(den) and num share v's axis and therefore commute. With
+// z = delta * Lambda and n2 = |Lambda|^2 / 4 per (d, k):
+//   N = max(1 - delta*a_L + delta^2 n2, eps),
+//   q = ((1 - delta^2 n2) / N, delta * v_L / N),
+// one reciprocal per (t, d, k).
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace mqc {
+
+constexpr int MODE_DL = 0;
+constexpr int MODE_Q = 1;
+constexpr int kSsmThreads = 256;
+
+// Raw bits of N consecutive storage elements (unpacked only on use).
+template <typename T, int N>
+struct Raw {
+  static constexpr int W = (N * (int)sizeof(T) + 3) / 4;
+  uint32_t w[W];
+};
+
+// Load N elements from a byte address (base + 32-bit lane offset).
+template <typename T, int N>
+__device__ inline void raw_load(const char* __restrict__ p, Raw<T, N>& r) {
+  constexpr int W = Raw<T, N>::W;
+  constexpr int bytes = N * (int)sizeof(T);
+  if constexpr (bytes % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) {
+      uint4 v = reinterpret_cast<const uint4*>(p)[i];
+      r.w[4 * i + 0] = v.x;
+      r.w[4 * i + 1] = v.y;
+      r.w[4 * i + 2] = v.z;
+      r.w[4 * i + 3] = v.w;
+    }
+  } else if constexpr (bytes == 8) {
+    uint2 v = *reinterpret_cast<const uint2*>(p);
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+  } else if constexpr (bytes == 4) {
+    r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else {
+    static_assert(bytes == 2, "unsupported raw width");
+    r.w[0] = *reinterpret_cast<const uint16_t*>(p);
+  }
+}
+
+template <typename T, int N>
+__device__ inline float raw_get(const Raw<T, N>& r, int e) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(r.w[e]);
+  } else if constexpr (std::is_same<T, bf16_t>::value) {
+    const uint32_t word = r.w[e >> 1];
+    return __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
+  } else {
+    const uint32_t word = r.w[e >> 1];
+    return io<T>::bits_to_f32((e & 1) ? (word >> 16) : (word & 0xffffu));
+  }
+}
+
+template <typename T, int N>
+__device__ inline quat raw_quat(const Raw<T, N>& r, int qi) {
+  return quat{raw_get(r, 4 * qi + 0), raw_get(r, 4 * qi + 1), raw_get(r, 4 * qi + 2),
+              raw_get(r, 4 * qi + 3)};
+}
+
+struct SsmArgs {
+  // MODE_DL: delta, s [B,T,D]; lam_alpha [D,S]; lam_imag [D,S,3]; dvec [D]
+  const void* delta;
+  const void* s;
+  const float* lam_alpha;
+  const float* lam_imag;
+  const float* dvec;
+  // MODE_Q: q [B,T,D,S,4]; Sq [B,T,D,4]; Dq strided [B,T,D]
+  const void* q;
+  const void* Sq;
+  const void* Dq;
+  int64_t d_sb, d_st, d_sd;
+  // both
+  const void* Bm;
+  const void* Cm;
+  const void* h0;
+  void* y;
+  void* h_last;
+  int64_t batch, T, Dm, S;
+  float eps;
+};
+
+template <typename T, int MODE, int KPL>
+struct Step;
+
+template <typename T, int KPL>
+struct Step<T, MODE_DL, KPL> {
+  Raw<T, 1> delta, s;
+  Raw<T, 4 * KPL> B, C;
+};
+
+template <typename T, int KPL>
+struct Step<T, MODE_Q, KPL> {
+  Raw<T, 4 * KPL> q, B, C;
+  Raw<T, 4> S;
+  Raw<T, 1> D;
+};
+
+// Sum `acc` over the G lanes of a group (G a power of two, groups aligned in
+// the wave). Returns, in v[0..NC), the components this lane ends up holding,
+// and the index of the first of them in c0 (they are consecutive).
+//   G == 1: all four, G == 2: two, G >= 4: one (component 2*(lane&1) + ((lane>>1)&1)),
+// valid in the group's first four lanes (for G <= 16 in every lane).
+template <int G>
+__device__ inline int group_reduce(const quat& acc, int lane, float (&v)[4], int& c0) {
+  if constexpr (G == 1) {
+    v[0] = acc.w; v[1] = acc.x; v[2] = acc.y; v[3] = acc.z;
+    c0 = 0;
+    return 4;
+  } else {
+    const bool odd = lane & 1;
+    // Stage 1 (lane ^ 1): even lanes keep components (0,1), odd lanes keep
+    // (2,3); each adds the partner's copy of the pair it keeps.
+    const float s0 = odd ? acc.w : acc.y;
+    const float s1 = odd ? acc.x : acc.z;
+    float k0 = odd ? acc.y : acc.w;
+    float k1 = odd ? acc.z : acc.x;
+    k0 += lane_xor1(s0);
+    k1 += lane_xor1(s1);
+    if constexpr (G == 2) {
+      v[0] = k0; v[1] = k1;
+      c0 = odd ? 2 : 0;
+      return 2;
+    } else {
+      // Stage 2 (lane ^ 2): lanes with bit 1 clear keep the first of the pair.
+      const bool hi = lane & 2;
+      const float snd = hi ? k0 : k1;
+      float kk = hi ? k1 : k0;
+      kk += lane_xor2(snd);
+      // Lanes holding the same component are 4 apart from here on.
+      if constexpr (G == 8) kk += __shfl_xor(kk, 4);
+      if constexpr (G >= 16) {
+        kk += row_rot4(kk);
+        kk += row_rot8(kk);
+      }
+      // Across rows the total lands in the group's first row, which holds the
+      // writer lanes (j < 4).
+      if constexpr (G >= 32) kk = sum_row_pair_to_even(kk);
+      if constexpr (G == 64) kk = sum_halves_to_low(kk);
+      v[0] = kk;
+      c0 = (odd ? 2 : 0) + (hi ? 1 : 0);
+      return 1;
+    }
+  }
+}
+
+__device__ inline float softplus_f(float x) {
+  // torch.nn.functional.softplus with beta = 1, threshold = 20.
+  return x > 20.f ? x : log1pf(expf(x));
+}
+
+// FULL: S == KPL * G, so every lane of a group owns real states.
+// SYNC: 0 = waves run freely; 1 = block barrier after every step; 2 = after
+// every PF steps.
+template <typename T, int MODE, int KPL, int G, int PF, int NT, bool FULL, int SYNC>
+__global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
+  static_assert((G & (G - 1)) == 0 && G <= 64 && NT % 64 == 0 && NT % G == 0,
+                "G must be a power of two <= 64 dividing the block");
+  constexpr int GPB = NT / G;  // groups (d's) per block
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int j = tid & (G - 1);
+  const int64_t b = blockIdx.y;
+  const int64_t d_raw = (int64_t)blockIdx.x * GPB + tid / G;
+  const bool gvalid = d_raw < a.Dm;
+  const int64_t d = gvalid ? d_raw : a.Dm - 1;
+  int k0 = j * KPL;
+  const bool kvalid = FULL || k0 < a.S;
+  if (!kvalid) k0 = (int)a.S - KPL;
+
+  const int64_t Tn = a.T;
+  const int64_t rowBC = a.Dm * a.S * 4;  // elements per (b, t) slice of B, C, q
+  const int64_t rowTok = a.Dm;           // elements per (b, t) slice of delta, s
+  // Byte offsets of this lane inside one (b, t) slice (the host checks that a
+  // slice is below 2 GiB).
+  const uint32_t offBC = (uint32_t)((d * a.S + k0) * 4 * (int64_t)sizeof(T));
+  const uint32_t offTok = (uint32_t)(d * (int64_t)sizeof(T));
+  const uint32_t offQ4 = (uint32_t)(d * 4 * (int64_t)sizeof(T));
+
+  // Per-(d,k) constants of the Cayley closed form (MODE_DL).
+  float la[KPL], ln2[KPL], lv[KPL][3];
+  float dskip = 0.f;
+  if constexpr (MODE == MODE_DL) {
+#pragma unroll
+    for (int kk = 0; kk < KPL; ++kk) {
+      const int64_t dk = d * a.S + k0 + kk;
+      const float ar = -softplus_f(a.lam_alpha[dk]);
+      const float v0 = tanhf(a.lam_imag[dk * 3 + 0]);
+      const float v1 = tanhf(a.lam_imag[dk * 3 + 1]);
+      const float v2 = tanhf(a.lam_imag[dk * 3 + 2]);
+      la[kk] = ar;
+      ln2[kk] = 0.25f * (ar * ar + v0 * v0 + v1 * v1 + v2 * v2);
+      lv[kk][0] = v0; lv[kk][1] = v1; lv[kk][2] = v2;
+    }
+    dskip = a.dvec[d];
+  }
+
+  // States.
+  quat h[KPL];
+#pragma unroll
+  for (int kk = 0; kk < KPL; ++kk) h[kk] = quat{0.f, 0.f, 0.f, 0.f};
+  if (a.h0) {
+    float e[4 * KPL];
+    load_vec<T, 4 * KPL>((const T*)a.h0 + ((b * a.Dm + d) * a.S + k0) * 4, e);
+#pragma unroll
+    for (int kk = 0; kk < KPL; ++kk) h[kk] = quat_from(&e[4 * kk]);
+  }
+
+  // Loads of step t into a ring slot; t is wave-uniform, so every slice base
+  // below is a scalar and the lane adds only its 32-bit offset.
+  auto load_step = [&](Step<T, MODE, KPL>& st, int64_t t) {
+    const int64_t rt = b * Tn + t;
+    if constexpr (MODE == MODE_DL) {
+      raw_load<T, 1>((const char*)((const T*)a.delta + rt * rowTok) + offTok, st.delta);
+      raw_load<T, 1>((const char*)((const T*)a.s + rt * rowTok) + offTok, st.s);
+    } else {
+      raw_load<T, 4>((const char*)((const T*)a.Sq + rt * rowTok * 4) + offQ4, st.S);
+      raw_load<T, 1>((const char*)((const T*)a.Dq + b * a.d_sb + t * a.d_st + d * a.d_sd), st.D);
+      raw_load<T, 4 * KPL>((const char*)((const T*)a.q + rt * rowBC) + offBC, st.q);
+    }
+    raw_load<T, 4 * KPL>((const char*)((const T*)a.Bm + rt * rowBC) + offBC, st.B);
+    raw_load<T, 4 * KPL>((const char*)((const T*)a.Cm + rt * rowBC) + offBC, st.C);
+  };
+
+  Step<T, MODE, KPL> ring[PF];
+  const int64_t t_last = Tn - 1;
+#pragma unroll
+  for (int i = 0; i < PF; ++i) load_step(ring[i], i < Tn ? i : t_last);
+
+  const bool writer = gvalid && (G < 4 || j < 4);
+  const int64_t rowY = a.Dm * 4;
+
+  for (int64_t t0 = 0; t0 < Tn; t0 += PF) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int64_t t = t0 + i;
+      if (t >= Tn) break;
+      Step<T, MODE, KPL>& cur = ring[i];
+
+      quat acc{0.f, 0.f, 0.f, 0.f};
+      float sv = 0.f;
+      float Sv[4] = {0.f, 0.f, 0.f, 0.f};
+      float Dv = 0.f;
+      if constexpr (MODE == MODE_DL) {
+        const float dl = raw_get(cur.delta, 0);
+        sv = raw_get(cur.s, 0);
+        const float dl2 = dl * dl;
+#pragma unroll
+        for (int kk = 0; kk < KPL; ++kk) {
+          float N = fmaf(dl2, ln2[kk], fmaf(-dl, la[kk], 1.f));
+          N = fmaxf(N, a.eps);
+          const float r = __builtin_amdgcn_rcpf(N);
+          const float c = dl * r;
+          const quat qd{fmaf(-dl2, ln2[kk], 1.f) * r, c * lv[kk][0], c * lv[kk][1],
+                        c * lv[kk][2]};
+          const quat Bk = raw_quat(cur.B, kk);
+          quat hn{sv * Bk.w, sv * Bk.x, sv * Bk.y, sv * Bk.z};
+          qmul_acc(hn, qd, h[kk]);
+          h[kk] = hn;
+          qmul_acc(acc, raw_quat(cur.C, kk), hn);
+        }
+      } else {
+        const quat Sq = raw_quat(cur.S, 0);
+        Sv[0] = Sq.w; Sv[1] = Sq.x; Sv[2] = Sq.y; Sv[3] = Sq.z;
+        Dv = raw_get(cur.D, 0);
+#pragma unroll
+        for (int kk = 0; kk < KPL; ++kk) {
+          const quat qk = raw_quat(cur.q, kk);
+          quat hn = qmul(raw_quat(cur.B, kk), Sq);
+          qmul_acc(hn, qk, h[kk]);
+          h[kk] = hn;
+          qmul_acc(acc, raw_quat(cur.C, kk), hn);
+        }
+      }
+      // Refill the consumed slot with step t + PF (clamped: the tail re-reads
+      // the last step, which keeps the loads unconditional).
+      {
+        const int64_t tn = t + PF;
+        load_step(cur, tn < Tn ? tn : t_last);
+      }
+      if constexpr (!FULL) {
+        if (!kvalid) acc = quat{0.f, 0.f, 0.f, 0.f};
+      }
+
+      float v[4];
+      int c0;
+      const int nc = group_reduce<G>(acc, lane, v, c0);
+      if (writer) {
+        T* yo = (T*)a.y + (b * Tn + t) * rowY + d * 4;
+        if constexpr (MODE == MODE_DL) {
+          if (c0 == 0) v[0] = fmaf(dskip, sv, v[0]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (e < nc) v[e] = fmaf(Dv, Sv[c0 + e], v[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (e < nc) store_scalar(yo + c0 + e, v[e]);
+      }
+      if constexpr (SYNC == 1) __syncthreads();
+    }
+    if constexpr (SYNC == 2) __syncthreads();
+  }
+
+  if (a.h_last && gvalid && kvalid) {
+    float e[4 * KPL];
+#pragma unroll
+    for (int kk = 0; kk < KPL; ++kk) {
+      e[4 * kk + 0] = h[kk].w; e[4 * kk + 1] = h[kk].x;
+      e[4 * kk + 2] = h[kk].y; e[4 * kk + 3] = h[kk].z;
+    }
+    store_vec<T, 4 * KPL>((T*)a.h_last + ((b * a.Dm + d) * a.S + k0) * 4, e);
+  }
+}
+
+// Steps of operands in flight per lane.
+template <typename T, int KPL>
+constexpr int ssm_prefetch() { return KPL * (int)sizeof(T) >= 8 ? 4 : 8; }
+
+template <typename T, int MODE, int KPL, int G, int PF = ssm_prefetch<T, KPL>(),
+          int NT = kSsmThreads, int SYNC = 0>
+int launch_ssm_g(const SsmArgs& a, hipStream_t s) {
+  constexpr int GPB = NT / G;
+  const int64_t gx = (a.Dm + GPB - 1) / GPB;
+  if (gx > 0x7fffffffLL || a.batch > 65535) return MQC_E_LIMIT;
+  const dim3 grid((unsigned)gx, (unsigned)a.batch);
+  if (a.S == (int64_t)KPL * G)
+    ssm_scan_kernel<T, MODE, KPL, G, PF, NT, true, SYNC><<<grid, dim3(NT), 0, s>>>(a);
+  else
+    ssm_scan_kernel<T, MODE, KPL, G, PF, NT, false, SYNC><<<grid, dim3(NT), 0, s>>>(a);
+  return launch_status();
+}
+
+// Block shape. The waves of a block run in lockstep (a barrier after every
+// step), so at any moment a block reads one contiguous span of each (b, t)
+// slice of B and C instead of scattered 1 KiB pieces at drifting t: DRAM row
+// locality, measured on MI355X at 4.76 -> 5.44 TB/s for the config-3 shape.
+// 768-thread blocks (12 waves: one block per CU at <= 168 VGPRs, 24 KiB of
+// each slice per step with G = 32) are used when there are enough of them to
+// give every CU one; smaller problems use 256-thread blocks.
+constexpr int kCUs = 256;  // MI355X compute units
+
+template <typename T, int MODE, int KPL, int G>
+int launch_ssm_shape(const SsmArgs& a, hipStream_t s) {
+  constexpr int PF = ssm_prefetch<T, KPL>();
+  if constexpr (G >= 8) {
+    constexpr int GPB = 768 / G;
+    if (a.batch * ((a.Dm + GPB - 1) / GPB) >= kCUs)
+      return launch_ssm_g<T, MODE, KPL, G, PF, 768, 1>(a, s);
+  }
+  return launch_ssm_g<T, MODE, KPL, G, PF, 256, 1>(a, s);
+}
+
+template <typename T, int MODE, int KPL>
+int launch_ssm_kpl(const SsmArgs& a, hipStream_t s) {
+  const int64_t per = (a.S + KPL - 1) / KPL;  // lanes needed per (b, d)
+  if (per <= 1) return launch_ssm_shape<T, MODE, KPL, 1>(a, s);
+  if (per <= 2) return launch_ssm_shape<T, MODE, KPL, 2>(a, s);
+  if (per <= 4) return launch_ssm_shape<T, MODE, KPL, 4>(a, s);
+  if (per <= 8) return launch_ssm_shape<T, MODE, KPL, 8>(a, s);
+  if (per <= 16) return launch_ssm_shape<T, MODE, KPL, 16>(a, s);
+  if (per <= 32) return launch_ssm_shape<T, MODE, KPL, 32>(a, s);
+  if (per <= 64) return launch_ssm_shape<T, MODE, KPL, 64>(a, s);
+  return MQC_E_LIMIT;
+}
+
+// Lane width: 16-byte loads of B and C where the layout allows (two states
+// per lane for 16-bit storage, one for fp32), wider lanes for d_state > 64.
+// KPL states per lane need d_state % KPL == 0 (lanes past the last k are
+// clamped onto the last KPL states).
+template <typename T, int MODE>
+int launch_ssm(const SsmArgs& a, hipStream_t s) {
+  if (a.batch == 0 || a.T == 0 || a.Dm == 0) return MQC_OK;
+  // Per-(b, t) slices are addressed with 32-bit lane offsets.
+  if (a.Dm * a.S * 4 * (int64_t)sizeof(T) >= ((int64_t)1 << 31)) return MQC_E_LIMIT;
+  const uintptr_t qa = 4 * sizeof(T);
+  if (!aligned(a.Bm, qa) || !aligned(a.Cm, qa) || !aligned(a.y, sizeof(T)) ||
+      (MODE == MODE_Q && (!aligned(a.q, qa) || !aligned(a.Sq, qa) || !aligned(a.Dq, sizeof(T)))) ||
+      (a.h0 && !aligned(a.h0, qa)) || (a.h_last && !aligned(a.h_last, qa)))
+    return MQC_E_ALIGN;
+  auto wide_ok = [&](int kpl) {
+    const uintptr_t al = kpl * 4 * sizeof(T) >= 16 ? 16 : kpl * 4 * sizeof(T);
+    return a.S % kpl == 0 && aligned(a.Bm, al) && aligned(a.Cm, al) &&
+           (MODE == MODE_DL || aligned(a.q, al)) && (!a.h0 || aligned(a.h0, al)) &&
+           (!a.h_last || aligned(a.h_last, al));
+  };
+  if constexpr (sizeof(T) == 2) {
+    if (a.S <= 128 && wide_ok(2)) return launch_ssm_kpl<T, MODE, 2>(a, s);
+    if (a.S <= 64) return launch_ssm_kpl<T, MODE, 1>(a, s);
+    if (a.S <= 256 && wide_ok(4)) return launch_ssm_kpl<T, MODE, 4>(a, s);
+    return MQC_E_LIMIT;
+  } else {
+    if (a.S <= 64) return launch_ssm_kpl<T, MODE, 1>(a, s);
+    if (a.S <= 128 && wide_ok(2)) return launch_ssm_kpl<T, MODE, 2>(a, s);
+    if (a.S <= 256 && wide_ok(4)) return launch_ssm_kpl<T, MODE, 4>(a, s);
+    return MQC_E_LIMIT;
+  }
+}
+
+// One translation unit per storage type instantiates these (ssm_scan_*.hip),
+// so the three compile in parallel.
+extern template int launch_ssm<float, MODE_DL>(const SsmArgs&, hipStream_t);
+extern template int launch_ssm<float, MODE_Q>(const SsmArgs&, hipStream_t);
+extern template int launch_ssm<bf16_t, MODE_DL>(const SsmArgs&, hipStream_t);
+extern template int launch_ssm<bf16_t, MODE_Q>(const SsmArgs&, hipStream_t);
+extern template int launch_ssm<f16_t, MODE_DL>(const SsmArgs&, hipStream_t);
+extern template int launch_ssm<f16_t, MODE_Q>(const SsmArgs&, hipStream_t);
+
+}  // namespace mqc
