@@ -120,6 +120,64 @@ int mqc_ssm_fused_fwd(const void* delta, const void* s, const void* B, const voi
 int mqc_qln_fwd(const void* q, const float* gamma, const float* beta, void* out, float* mean,
                 float* rstd, int64_t rows, int64_t d, float eps, int dtype, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Training: forward with state checkpoints, and the backward passes.
+ * The reference has no backward for any of its GPU kernels (its Triton launches
+ * sit outside autograd); these entry points serve torch.autograd.Function
+ * wrappers whose gradients equal autograd through the reference's CPU path
+ * (models/quaternion_mamba2_block.py:124-230 with kernels/ssm_fused.py:405-430,
+ * kernels/quaternion_norm.py:219-245).
+ * ------------------------------------------------------------------------- */
+
+/* Checkpoint interval K that mqc_ssm_fused_bwd requires for `dtype` (the
+ * backward keeps K steps of operands and states in registers). */
+int mqc_ssm_bwd_ckpt_every(int dtype);
+
+/* mqc_ssm_fused_fwd plus fp32 state checkpoints for the backward:
+ * h_ckpt [batch, ceil(seq_len / ckpt_every), d_inner, d_state, 4] receives the
+ * state at the last step of every chunk of ckpt_every steps (the last chunk may
+ * be shorter). */
+int mqc_ssm_fused_fwd_train(const void* delta, const void* s, const void* B, const void* C,
+                            const float* lambda_alpha, const float* lambda_imag, const float* D,
+                            const void* h0, void* y, void* h_last, float* h_ckpt,
+                            int64_t ckpt_every, int64_t batch, int64_t seq_len, int64_t d_inner,
+                            int64_t d_state, float eps, int dtype, void* stream);
+
+/* Backward of mqc_ssm_fused_fwd_train given gy = dL/dy (dtype [batch, seq_len,
+ * d_inner, 4]) and optionally dh_last = dL/dh_last (dtype [batch, d_inner,
+ * d_state, 4]). Writes d_delta, d_s (fp32 [batch, seq_len, d_inner]: these
+ * sums over d_state keep fp32 precision for callers whose delta is fp32, as
+ * under autocast), dB, dC (dtype, shape of B), per-batch partial parameter gradients
+ * dlambda_alpha_part fp32 [batch, d_inner, d_state],
+ * dlambda_imag_part fp32 [batch, d_inner, d_state, 3], dD_part fp32
+ * [batch, d_inner] (the caller sums them over batch), and dh0 (dtype
+ * [batch, d_inner, d_state, 4]) if non-NULL. h0 and h_ckpt must be the forward's;
+ * ckpt_every must equal mqc_ssm_bwd_ckpt_every(dtype); d_state <= 64. */
+int mqc_ssm_fused_bwd(const void* delta, const void* s, const void* B, const void* C,
+                      const float* lambda_alpha, const float* lambda_imag, const float* D,
+                      const void* h0, const float* h_ckpt, int64_t ckpt_every, const void* gy,
+                      const void* dh_last, float* d_delta, float* d_s, void* dB, void* dC,
+                      float* dlambda_alpha_part, float* dlambda_imag_part, float* dD_part,
+                      void* dh0, int64_t batch, int64_t seq_len, int64_t d_inner,
+                      int64_t d_state, float eps, int dtype, void* stream);
+
+/* Backward of mqc_qln_fwd given dout (dtype [rows, d, 4]) and the forward's
+ * saved mean and rstd: writes dq (dtype [rows, d, 4]) and
+ * ne = n-hat * <dout, q / (n + eps)> (fp32 [rows, d]); dgamma = sum over rows
+ * of ne and dbeta = sum over rows of dout are left to the caller. */
+int mqc_qln_bwd(const void* q, const void* dout, const float* gamma, const float* mean,
+                const float* rstd, void* dq, float* ne, int64_t rows, int64_t d, float eps,
+                int dtype, void* stream);
+
+/* Backward of mqc_out_gate_fwd (dx = dout is the caller's). z is read as in the
+ * forward (first `cols` columns, rows z_row_stride apart); dz (dtype, dense
+ * [rows, z_cols], z_cols >= cols) = dout * y_real * sigmoid'(z) in the first
+ * `cols` columns and 0 after them; dy_real (dtype [rows, cols]) =
+ * dout * sigmoid(z). */
+int mqc_out_gate_bwd(const void* dout, const void* z, int64_t z_row_stride, const void* y_real,
+                     void* dz, void* dy_real, int64_t rows, int64_t cols, int64_t z_cols,
+                     int dtype, void* stream);
+
 /* Output step epilogue of the block: out = x + sigmoid(z) * y_real, where
  * x, y_real, out: dtype [rows, cols] contiguous and z: dtype with element
  * (r, c) at z[r * z_row_stride + c] (the gate half of in_proj's output).

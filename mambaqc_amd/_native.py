@@ -41,7 +41,16 @@ SIGNATURES = {
                           _i64, _i64, _i64, _i64, _f32, _int, _vp],
     "mqc_qln_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _int, _vp],
     "mqc_out_gate_fwd": [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _int, _vp],
+    "mqc_ssm_bwd_ckpt_every": [_int],
+    "mqc_ssm_fused_fwd_train": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                                _i64, _i64, _i64, _i64, _f32, _int, _vp],
+    "mqc_ssm_fused_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
+                          _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _int, _vp],
+    "mqc_qln_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _int, _vp],
+    "mqc_out_gate_bwd": [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
 }
+
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib = None
@@ -73,8 +82,9 @@ def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
         lib.mqc_status_string.restype = ctypes.c_char_p
         lib.mqc_abi_version.argtypes = []
         lib.mqc_abi_version.restype = _int
-        if lib.mqc_abi_version() != 1:
-            raise NativeLibraryMissing(f"{p}: ABI version {lib.mqc_abi_version()} != 1; rebuild")
+        if lib.mqc_abi_version() != ABI_VERSION:
+            raise NativeLibraryMissing(
+                f"{p}: ABI version {lib.mqc_abi_version()} != {ABI_VERSION}; rebuild")
         if path is None:
             _lib = lib
         return lib

@@ -14,7 +14,10 @@ under the same seed, identical state_dict keys), and the same forward:
     out = x + sigmoid(z[..., :d_model]) * y_real            HIP: mqc_out_gate_fwd
 
 z, q and the quaternion S are never materialised: the SSM kernel discretises
-in registers and takes the real selected signal s.
+in registers and takes the real selected signal s. When autograd is recording,
+the SSM, QLN and gate run as torch.autograd.Functions with HIP backward
+kernels (the reference's GPU path has no backward: its Triton launches sit
+outside autograd); the GEMMs, conv and activations use torch's autograd.
 
 The gate uses z[..., :d_model]. The reference multiplies sigmoid(z), which has
 d_inner = expand_factor * d_model features, by y_real, which has d_model
@@ -36,27 +39,68 @@ from .layers.causal_conv1d import CausalConv1d
 from .layers.quaternion_linear import quaternion_to_real_projection, real_to_quaternion_projection
 
 
+def _gate_operands(x, z, y_real):
+    """Operands in the result dtype: torch's promotion of x, z and y_real, as in
+    the reference's x + sigmoid(z) * y_real (an fp32 residual stream under fp16
+    autocast stays fp32)."""
+    d = x.shape[-1]
+    dtype = torch.promote_types(torch.promote_types(x.dtype, z.dtype), y_real.dtype)
+    x = nat.aligned16(x.detach().to(dtype))
+    z = z.detach().to(dtype)
+    if z.stride(-1) != 1 or (z.dim() > 1 and not _rows_uniform(z)):
+        z = z[..., :d].contiguous()
+    y_real = nat.aligned16(y_real.detach().to(dtype))
+    rows = x.numel() // d if d else 0
+    zs = z.stride(-2) if z.dim() > 1 else z.shape[-1]
+    return x, z, zs, y_real, rows, d
+
+
+class _OutGateFunction(torch.autograd.Function):
+    """out = x + sigmoid(z[..., :d]) * y_real with a HIP backward."""
+
+    @staticmethod
+    def forward(ctx, x, z, y_real):
+        xc, zc, zs, yc, rows, d = _gate_operands(x, z, y_real)
+        out = torch.empty_like(xc)
+        nat.call("mqc_out_gate_fwd", xc, xc.data_ptr(), zc.data_ptr(), zs, yc.data_ptr(),
+                 out.data_ptr(), rows, d, nat.dtype_code(xc), nat.stream_of(xc))
+        ctx.save_for_backward(zc, yc)
+        ctx.meta = (zs, rows, d, tuple(z.shape), x.dtype, z.dtype, y_real.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        zc, yc = ctx.saved_tensors
+        zs, rows, d, zshape, t_x, t_z, t_y = ctx.meta
+        dout = nat.aligned16(dout.to(yc.dtype))
+        zcols = zshape[-1]
+        dz = torch.empty(zshape, device=yc.device, dtype=yc.dtype)
+        dy = torch.empty_like(yc)
+        # zc may have been narrowed to the first d columns: its gradient beyond
+        # d is zero either way.
+        nat.call("mqc_out_gate_bwd", yc, dout.data_ptr(), zc.data_ptr(), zs, yc.data_ptr(),
+                 dz.data_ptr(), dy.data_ptr(), rows, d, zcols, nat.dtype_code(yc),
+                 nat.stream_of(yc))
+        return dout.to(t_x), dz.to(t_z), dy.to(t_y)
+
+
 def out_gate(x: torch.Tensor, z: torch.Tensor, y_real: torch.Tensor) -> torch.Tensor:
     """x + sigmoid(z[..., :d]) * y_real for x, y_real [..., d] and z [..., >= d].
 
     z may be a strided view whose last axis is contiguous (the gate half of
-    in_proj's output); it is read in place.
+    in_proj's output); it is read in place. Differentiable when autograd is
+    recording.
     """
     d = x.shape[-1]
     assert y_real.shape == x.shape, f"y_real {tuple(y_real.shape)} vs x {tuple(x.shape)}"
     assert z.shape[:-1] == x.shape[:-1] and z.shape[-1] >= d
     nat.require_device("out_gate", x, z, y_real)
-    dtype = y_real.dtype
-    x = nat.aligned16(x.to(dtype))
-    z = z.to(dtype)
-    if z.stride(-1) != 1 or (z.dim() > 1 and not _rows_uniform(z)):
-        z = z[..., :d].contiguous()
-    y_real = nat.aligned16(y_real)
-    rows = x.numel() // d if d else 0
-    zs = z.stride(-2) if z.dim() > 1 else z.shape[-1]
-    out = torch.empty_like(x)
-    nat.call("mqc_out_gate_fwd", x, x.data_ptr(), z.data_ptr(), zs, y_real.data_ptr(),
-             out.data_ptr(), rows, d, nat.dtype_code(x), nat.stream_of(x))
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (x, z, y_real)):
+        return _OutGateFunction.apply(x, z, y_real)
+    xc, zc, zs, yc, rows, d = _gate_operands(x, z, y_real)
+    out = torch.empty_like(xc)
+    nat.call("mqc_out_gate_fwd", xc, xc.data_ptr(), zc.data_ptr(), zs, yc.data_ptr(),
+             out.data_ptr(), rows, d, nat.dtype_code(xc), nat.stream_of(xc))
     return out
 
 
@@ -97,10 +141,6 @@ class QuaternionMamba2Block(nn.Module):
         self.out_proj = quaternion_to_real_projection(D, d_model, bias=bias)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
-            raise NotImplementedError(
-                "QuaternionMamba2Block (mambaqc_amd) has no backward yet; run the forward under "
-                "torch.no_grad() or torch.inference_mode()")
         xz = self.in_proj(x)
         x_in, z = xz.chunk(2, dim=-1)
         x_act = F.silu(self.conv1d(x_in))

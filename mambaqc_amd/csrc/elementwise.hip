@@ -235,6 +235,46 @@ int launch_out_gate(const void* x, const void* z, int64_t zs, const void* y, voi
   return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// Backward of out = x + sigmoid(z[:, :cols]) * y (dx = dout is the caller's):
+//   dz[r, c] = dout * y * sig (1 - sig)  for c < cols, 0 for cols <= c < z_cols
+//   dy[r, c] = dout * sig
+// z is read with row stride zs; dz is written dense [rows, z_cols].
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kThreads) void out_gate_bwd_kernel(
+    const T* __restrict__ dout, const T* __restrict__ z, int64_t zs, const T* __restrict__ y,
+    T* __restrict__ dz, T* __restrict__ dy, int64_t rows, int64_t cols, int64_t zcols) {
+  const int64_t n = rows * zcols;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / zcols;
+    const int64_t c = i - r * zcols;
+    if (c < cols) {
+      const float go = load_scalar(dout + r * cols + c);
+      const float sg = 1.f / (1.f + __expf(-load_scalar(z + r * zs + c)));
+      const float yv = load_scalar(y + r * cols + c);
+      store_scalar(dz + i, go * yv * sg * (1.f - sg));
+      store_scalar(dy + r * cols + c, go * sg);
+    } else {
+      store_scalar(dz + i, 0.f);
+    }
+  }
+}
+
+template <typename T>
+int launch_out_gate_bwd(const void* dout, const void* z, int64_t zs, const void* y, void* dz,
+                        void* dy, int64_t rows, int64_t cols, int64_t zcols, hipStream_t s) {
+  if (rows == 0 || zcols == 0) return MQC_OK;
+  if (!aligned(dout, sizeof(T)) || !aligned(z, sizeof(T)) || !aligned(y, sizeof(T)) ||
+      !aligned(dz, sizeof(T)) || !aligned(dy, sizeof(T)))
+    return MQC_E_ALIGN;
+  out_gate_bwd_kernel<T><<<dim3((unsigned)grid_for(rows * zcols, kThreads)), dim3(kThreads), 0,
+                           s>>>((const T*)dout, (const T*)z, zs, (const T*)y, (T*)dz, (T*)dy,
+                                rows, cols, zcols);
+  return launch_status();
+}
+
 }  // namespace mqc
 
 using namespace mqc;
@@ -253,7 +293,7 @@ const char* mqc_status_string(int status) {
   }
 }
 
-int mqc_abi_version(void) { return 1; }
+int mqc_abi_version(void) { return 2; }
 
 int mqc_quaternion_multiply(const void* p, const void* q, void* out, int64_t n_quat, int dtype,
                             void* stream) {
@@ -282,6 +322,23 @@ int mqc_quaternion_norm(const void* q, void* out, int64_t n_quat, int dtype, voi
     case MQC_F32: return launch_norm<float>(q, out, n_quat, s);
     case MQC_BF16: return launch_norm<bf16_t>(q, out, n_quat, s);
     case MQC_F16: return launch_norm<f16_t>(q, out, n_quat, s);
+    default: return MQC_E_DTYPE;
+  }
+}
+
+int mqc_out_gate_bwd(const void* dout, const void* z, int64_t z_row_stride, const void* y_real,
+                     void* dz, void* dy_real, int64_t rows, int64_t cols, int64_t z_cols,
+                     int dtype, void* stream) {
+  if (rows < 0 || cols < 0 || z_cols < cols || z_row_stride < cols) return MQC_E_SHAPE;
+  if (rows > 0 && z_cols > 0 && (!dout || !z || !y_real || !dz || !dy_real)) return MQC_E_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MQC_F32:
+      return launch_out_gate_bwd<float>(dout, z, z_row_stride, y_real, dz, dy_real, rows, cols, z_cols, s);
+    case MQC_BF16:
+      return launch_out_gate_bwd<bf16_t>(dout, z, z_row_stride, y_real, dz, dy_real, rows, cols, z_cols, s);
+    case MQC_F16:
+      return launch_out_gate_bwd<f16_t>(dout, z, z_row_stride, y_real, dz, dy_real, rows, cols, z_cols, s);
     default: return MQC_E_DTYPE;
   }
 }

@@ -1,0 +1,76 @@
+// C ABI of the fused quaternion SSM's training forward (state checkpoints) and
+// backward (kernels: ssm_scan.hpp, ssm_bwd.hpp).
+#include "ssm_bwd.hpp"
+
+using namespace mqc;
+
+extern "C" {
+
+int mqc_ssm_bwd_ckpt_every(int dtype) {
+  switch (dtype) {
+    case MQC_F32: return ssm_bwd_chunk<float>();
+    case MQC_BF16: return ssm_bwd_chunk<bf16_t>();
+    case MQC_F16: return ssm_bwd_chunk<f16_t>();
+    default: return MQC_E_DTYPE;
+  }
+}
+
+int mqc_ssm_fused_fwd_train(const void* delta, const void* s, const void* B, const void* C,
+                            const float* lambda_alpha, const float* lambda_imag, const float* D,
+                            const void* h0, void* y, void* h_last, float* h_ckpt,
+                            int64_t ckpt_every, int64_t batch, int64_t seq_len, int64_t d_inner,
+                            int64_t d_state, float eps, int dtype, void* stream) {
+  if (batch < 0 || seq_len < 0 || d_inner < 0 || d_state < 0 || ckpt_every < 1)
+    return MQC_E_SHAPE;
+  if (dtype != MQC_F32 && dtype != MQC_BF16 && dtype != MQC_F16) return MQC_E_DTYPE;
+  const bool work = batch > 0 && d_inner > 0 && seq_len > 0;
+  if (work && d_state == 0) return MQC_E_SHAPE;
+  if (work && (!delta || !s || !B || !C || !lambda_alpha || !lambda_imag || !D || !y || !h_ckpt))
+    return MQC_E_NULL;
+  if (batch > 65535 || d_inner > (1LL << 24) || d_state > 256) return MQC_E_LIMIT;
+  if (h_ckpt && !aligned(h_ckpt, 16)) return MQC_E_ALIGN;
+  SsmArgs a{};
+  a.delta = delta; a.s = s; a.lam_alpha = lambda_alpha; a.lam_imag = lambda_imag; a.dvec = D;
+  a.Bm = B; a.Cm = C; a.h0 = h0; a.y = y; a.h_last = h_last;
+  a.h_ckpt = h_ckpt; a.ckpt_every = ckpt_every;
+  a.batch = batch; a.T = seq_len; a.Dm = d_inner; a.S = d_state; a.eps = eps;
+  if (!work) return MQC_OK;
+  switch (dtype) {
+    case MQC_F32: return launch_ssm<float, MODE_DL>(a, (hipStream_t)stream);
+    case MQC_BF16: return launch_ssm<bf16_t, MODE_DL>(a, (hipStream_t)stream);
+    default: return launch_ssm<f16_t, MODE_DL>(a, (hipStream_t)stream);
+  }
+}
+
+int mqc_ssm_fused_bwd(const void* delta, const void* s, const void* B, const void* C,
+                      const float* lambda_alpha, const float* lambda_imag, const float* D,
+                      const void* h0, const float* h_ckpt, int64_t ckpt_every, const void* gy,
+                      const void* dh_last, float* d_delta, float* d_s, void* dB, void* dC,
+                      float* dlambda_alpha_part, float* dlambda_imag_part, float* dD_part,
+                      void* dh0, int64_t batch, int64_t seq_len, int64_t d_inner,
+                      int64_t d_state, float eps, int dtype, void* stream) {
+  if (batch < 0 || seq_len < 0 || d_inner < 0 || d_state < 0) return MQC_E_SHAPE;
+  if (dtype != MQC_F32 && dtype != MQC_BF16 && dtype != MQC_F16) return MQC_E_DTYPE;
+  const bool work = batch > 0 && d_inner > 0 && seq_len > 0;
+  if (work && d_state == 0) return MQC_E_SHAPE;
+  if (work && (!delta || !s || !B || !C || !lambda_alpha || !lambda_imag || !D || !h_ckpt ||
+               !gy || !d_delta || !d_s || !dB || !dC || !dlambda_alpha_part ||
+               !dlambda_imag_part || !dD_part))
+    return MQC_E_NULL;
+  if (batch > 65535 || d_inner > (1LL << 24) || d_state > 64) return MQC_E_LIMIT;
+  if (ckpt_every != mqc_ssm_bwd_ckpt_every(dtype)) return MQC_E_LIMIT;
+  SsmBwdArgs a{};
+  a.delta = delta; a.s = s; a.Bm = B; a.Cm = C; a.lam_alpha = lambda_alpha;
+  a.lam_imag = lambda_imag; a.dvec = D; a.h0 = h0; a.h_ckpt = h_ckpt; a.gy = gy;
+  a.dh_last = dh_last; a.d_delta = d_delta; a.d_s = d_s; a.dB = dB; a.dC = dC;
+  a.dalpha_part = dlambda_alpha_part; a.dimag_part = dlambda_imag_part; a.dD_part = dD_part;
+  a.dh0 = dh0; a.batch = batch; a.T = seq_len; a.Dm = d_inner; a.S = d_state; a.eps = eps;
+  if (!work) return MQC_OK;
+  switch (dtype) {
+    case MQC_F32: return launch_ssm_bwd<float>(a, (hipStream_t)stream);
+    case MQC_BF16: return launch_ssm_bwd<bf16_t>(a, (hipStream_t)stream);
+    default: return launch_ssm_bwd<f16_t>(a, (hipStream_t)stream);
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,295 @@
+// Backward of the block's fused quaternion SSM (delta-lambda form).
+//
+// Forward (ssm_scan.hpp), per lane (b, d, k):
+//   q_t = Cayley(delta_t * Lambda)          Lambda = (-softplus(alpha), tanh(imag))
+//   h_t = q_t (x) h_{t-1} + s_t * B_t
+//   y_t = sum_k C_t (x) h_t + (D * s_t, 0, 0, 0)
+// With r = p (x) q, dp = dr (x) conj(q) and dq = conj(p) (x) dr. Walking t backwards
+// with g_t = dL/dh_t:
+//   g_t      = conj(C_t) (x) gy_t + conj(q_{t+1}) (x) g_{t+1}      (g_T = dL/dh_last)
+//   dC_t     = gy_t (x) conj(h_t)
+//   dq_t     = g_t (x) conj(h_{t-1})
+//   dB_t     = s_t * g_t
+//   ds_t     = sum_k <g_t, B_t> + D * gy_t.w,   dD += gy_t.w * s_t
+//   dh0      = conj(q_0) (x) g_0
+// and dq_t is pulled back through the Cayley closed form (see cayley_pullback)
+// to d delta_t (summed over k) and to dalpha, dimag (summed over t here, over b
+// by the caller).
+//
+// States are not stored by the forward: it saves fp32 checkpoints of h at the
+// end of every chunk of K steps. The backward walks the chunks from last to
+// first; for each it reloads the chunk's operands, recomputes the chunk's K
+// states from the previous checkpoint into registers (same arithmetic as the
+// forward), then runs the adjoint steps above in reverse. One lane owns one
+// (b, d, k); a group of G lanes owns a (b, d) and sums d delta and ds over k
+// with the same VALU reduction as the forward. 768-thread blocks run in
+// lockstep (a barrier per chunk), like the forward.
+#pragma once
+
+#include "ssm_scan.hpp"
+
+namespace mqc {
+
+struct SsmBwdArgs {
+  const void* delta;  // [B,T,D] dtype
+  const void* s;      // [B,T,D] dtype
+  const void* Bm;     // [B,T,D,S,4] dtype
+  const void* Cm;     // [B,T,D,S,4] dtype
+  const float* lam_alpha;  // [D,S]
+  const float* lam_imag;   // [D,S,3]
+  const float* dvec;       // [D]
+  const void* h0;          // [B,D,S,4] dtype or null
+  const float* h_ckpt;     // [B,nC,D,S,4] fp32
+  const void* gy;          // [B,T,D,4] dtype
+  const void* dh_last;     // [B,D,S,4] dtype or null
+  float* d_delta;          // [B,T,D] fp32
+  float* d_s;              // [B,T,D] fp32
+  void* dB;                // [B,T,D,S,4] dtype
+  void* dC;                // [B,T,D,S,4] dtype
+  float* dalpha_part;      // [B,D,S]
+  float* dimag_part;       // [B,D,S,3]
+  float* dD_part;          // [B,D]
+  void* dh0;               // [B,D,S,4] dtype or null
+  int64_t batch, T, Dm, S;
+  float eps;
+};
+
+// Pull dq back through q = Cayley(dl * Lambda) (closed form, see ssm_scan.hpp):
+//   N = 1 - dl a + dl^2 n2 (clamped below at eps), P = 1 - dl^2 n2,
+//   q0 = P / N,  qv = dl v / N.
+// Returns d dl; accumulates the gradients w.r.t. a and v into da, dv. When the
+// clamp engages N is constant, as in the reference's clamp_min.
+__device__ inline float cayley_pullback(const quat& g, const quat& q, float dl, float dl2,
+                                        const LamConst& L, float eps, float& da, float (&dv)[3]) {
+  const float Nraw = fmaf(dl2, L.n2, fmaf(-dl, L.a, 1.f));
+  const float live = Nraw > eps ? 1.f : 0.f;
+  const float r = __builtin_amdgcn_rcpf(fmaxf(Nraw, eps));
+  const float gq = g.w * q.w + g.x * q.x + g.y * q.y + g.z * q.z;   // <dq, q>
+  const float gv = g.x * L.v0 + g.y * L.v1 + g.z * L.v2;            // <dq_vec, v>
+  const float gql = gq * live;
+  // d/d dl: dP = -2 dl n2, dN = -a + 2 dl n2
+  const float ddl = (g.w * (-2.f * dl * L.n2) + gv - gql * fmaf(2.f * dl, L.n2, -L.a)) * r;
+  // d/da: dP = -dl^2 a / 2, dN = -dl + dl^2 a / 2
+  const float h = 0.5f * dl2;
+  da += (g.w * (-h * L.a) - gql * fmaf(h, L.a, -dl)) * r;
+  // d/dv_i: dP = -dl^2 v_i / 2, dN = dl^2 v_i / 2, d(dl v_j) = dl [i == j]
+  const float cv = -h * (g.w + gql);
+  dv[0] += fmaf(cv, L.v0, dl * g.x) * r;
+  dv[1] += fmaf(cv, L.v1, dl * g.y) * r;
+  dv[2] += fmaf(cv, L.v2, dl * g.z) * r;
+  return ddl;
+}
+
+__device__ inline quat qconj(const quat& q) { return quat{q.w, -q.x, -q.y, -q.z}; }
+
+__device__ inline void qacc(quat& a, const quat& b) {
+  a.w += b.w; a.x += b.x; a.y += b.y; a.z += b.z;
+}
+
+// Sum two scalars over the G lanes of a group. Afterwards the group's lane 0
+// holds the total of u and lane 1 the total of w (G >= 2); for G == 1 the one
+// lane holds both (u in u, w in w).
+template <int G>
+__device__ inline void group_reduce2(float& u, float& w, int lane) {
+  if constexpr (G == 1) {
+    return;
+  } else {
+    const bool odd = lane & 1;
+    float keep = odd ? w : u;
+    const float snd = odd ? u : w;
+    keep += lane_xor1(snd);
+    if constexpr (G >= 4) keep += lane_xor2(keep);
+    if constexpr (G == 8) keep += __shfl_xor(keep, 4);
+    if constexpr (G >= 16) {
+      keep += row_rot4(keep);
+      keep += row_rot8(keep);
+    }
+    if constexpr (G >= 32) keep = sum_row_pair_to_even(keep);
+    if constexpr (G == 64) keep = sum_halves_to_low(keep);
+    u = keep;
+    w = keep;
+  }
+}
+
+template <typename T, int G, int K, int NT, bool FULL>
+__global__ __launch_bounds__(NT) void ssm_bwd_kernel(SsmBwdArgs a) {
+  static_assert((G & (G - 1)) == 0 && G <= 64 && NT % 64 == 0 && NT % G == 0, "bad group");
+  constexpr int GPB = NT / G;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int j = tid & (G - 1);
+  const int64_t b = blockIdx.y;
+  const int64_t d_raw = (int64_t)blockIdx.x * GPB + tid / G;
+  const bool gvalid = d_raw < a.Dm;
+  const int64_t d = gvalid ? d_raw : a.Dm - 1;
+  const bool kvalid = FULL || j < a.S;
+  const int64_t k = kvalid ? j : a.S - 1;
+  const bool own = gvalid && kvalid;
+
+  const int64_t Tn = a.T;
+  const int64_t nC = (Tn + K - 1) / K;
+  const int64_t rowBC = a.Dm * a.S * 4;
+  const int64_t rowTok = a.Dm;
+  const int64_t rowY = a.Dm * 4;
+  const uint32_t offBC = (uint32_t)((d * a.S + k) * 4 * (int64_t)sizeof(T));
+  const uint32_t offTok = (uint32_t)(d * (int64_t)sizeof(T));
+  const uint32_t offY = (uint32_t)(d * 4 * (int64_t)sizeof(T));
+  const int64_t sidx = ((b * a.Dm + d) * a.S + k) * 4;  // this lane's [B,D,S,4] index
+
+  const int64_t dk = d * a.S + k;
+  const LamConst L = lam_const(a.lam_alpha, a.lam_imag, dk);
+  const float Dv = a.dvec[d];
+
+  float da = 0.f, dv[3] = {0.f, 0.f, 0.f}, dD = 0.f;
+  quat carry{0.f, 0.f, 0.f, 0.f};
+  if (a.dh_last) {
+    float e[4];
+    load_vec<T, 4>((const T*)a.dh_last + sidx, e);
+    carry = quat_from(e);
+  }
+
+  for (int64_t c = nC - 1; c >= 0; --c) {
+    const int64_t t0 = c * K;
+    const int len = (int)(Tn - t0 < K ? Tn - t0 : K);
+    // Operands of the chunk (the tail chunk re-reads its last step).
+    Raw<T, 1> rd[K], rs[K];
+    Raw<T, 4> rB[K], rC[K], rg[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const int64_t rt = b * Tn + t0 + (i < len ? i : len - 1);
+      raw_load<T, 1>((const char*)((const T*)a.delta + rt * rowTok) + offTok, rd[i]);
+      raw_load<T, 1>((const char*)((const T*)a.s + rt * rowTok) + offTok, rs[i]);
+      raw_load<T, 4>((const char*)((const T*)a.Bm + rt * rowBC) + offBC, rB[i]);
+      raw_load<T, 4>((const char*)((const T*)a.Cm + rt * rowBC) + offBC, rC[i]);
+      raw_load<T, 4>((const char*)((const T*)a.gy + rt * rowY) + offY, rg[i]);
+    }
+    // State before the chunk: the previous chunk's checkpoint, or h0.
+    quat hs[K + 1];
+    if (c > 0) {
+      const float4 v = *reinterpret_cast<const float4*>(
+          a.h_ckpt + (((b * nC + (c - 1)) * a.Dm + d) * a.S + k) * 4);
+      hs[0] = quat{v.x, v.y, v.z, v.w};
+    } else if (a.h0) {
+      float e[4];
+      load_vec<T, 4>((const T*)a.h0 + sidx, e);
+      hs[0] = quat_from(e);
+    } else {
+      hs[0] = quat{0.f, 0.f, 0.f, 0.f};
+    }
+    // Recompute the chunk's states.
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      if (i < len) {
+        const float dl = raw_get(rd[i], 0);
+        const quat q = cayley_step(dl, dl * dl, L, a.eps);
+        hs[i + 1] = state_step(q, hs[i], raw_get(rs[i], 0), raw_quat(rB[i], 0));
+      }
+    }
+    // Adjoint steps, last to first.
+#pragma unroll
+    for (int i = K - 1; i >= 0; --i) {
+      if (i < len) {
+        const int64_t rt = b * Tn + t0 + i;
+        const float dl = raw_get(rd[i], 0);
+        const float dl2 = dl * dl;
+        const float sv = raw_get(rs[i], 0);
+        const quat q = cayley_step(dl, dl2, L, a.eps);
+        const quat gy = raw_quat(rg[i], 0);
+        const quat Ck = raw_quat(rC[i], 0);
+        const quat Bk = raw_quat(rB[i], 0);
+        quat g = carry;
+        qmul_acc(g, qconj(Ck), gy);
+        quat dq{0.f, 0.f, 0.f, 0.f};
+        qmul_acc(dq, g, qconj(hs[i]));
+        quat dC{0.f, 0.f, 0.f, 0.f};
+        qmul_acc(dC, gy, qconj(hs[i + 1]));
+        float ddl = cayley_pullback(dq, q, dl, dl2, L, a.eps, da, dv);
+        float dsk = g.w * Bk.w + g.x * Bk.x + g.y * Bk.y + g.z * Bk.z;
+        carry = quat{0.f, 0.f, 0.f, 0.f};
+        qmul_acc(carry, qconj(q), g);
+        if (own) {
+          const float eB[4] = {sv * g.w, sv * g.x, sv * g.y, sv * g.z};
+          const float eC[4] = {dC.w, dC.x, dC.y, dC.z};
+          store_vec<T, 4>((T*)a.dB + rt * rowBC + (d * a.S + k) * 4, eB);
+          store_vec<T, 4>((T*)a.dC + rt * rowBC + (d * a.S + k) * 4, eC);
+        } else {
+          ddl = 0.f;
+          dsk = 0.f;
+        }
+        group_reduce2<G>(ddl, dsk, lane);
+        if (gvalid) {
+          if (j == 0) a.d_delta[rt * rowTok + d] = ddl;
+          if (j == (G > 1 ? 1 : 0)) {
+            a.d_s[rt * rowTok + d] = fmaf(Dv, gy.w, dsk);
+            dD = fmaf(gy.w, sv, dD);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if (own) {
+    if (a.dh0) {
+      const float e[4] = {carry.w, carry.x, carry.y, carry.z};
+      store_vec<T, 4>((T*)a.dh0 + sidx, e);
+    }
+    // Chain to the raw parameters: a = -softplus(alpha), v = tanh(imag).
+    const float alpha = a.lam_alpha[dk];
+    const float sig = alpha > 20.f ? 1.f : 1.f / (1.f + expf(-alpha));
+    a.dalpha_part[b * a.Dm * a.S + dk] = -da * sig;
+    float* di = a.dimag_part + (b * a.Dm * a.S + dk) * 3;
+    di[0] = dv[0] * (1.f - L.v0 * L.v0);
+    di[1] = dv[1] * (1.f - L.v1 * L.v1);
+    di[2] = dv[2] * (1.f - L.v2 * L.v2);
+  }
+  if (gvalid && j == (G > 1 ? 1 : 0)) a.dD_part[b * a.Dm + d] = dD;
+}
+
+// Checkpoint interval the backward needs: the chunk's operands and states live
+// in registers, K steps at a time.
+template <typename T>
+constexpr int ssm_bwd_chunk() { return sizeof(T) == 4 ? 4 : 8; }
+
+template <typename T, int G>
+int launch_ssm_bwd_g(const SsmBwdArgs& a, hipStream_t s) {
+  constexpr int K = ssm_bwd_chunk<T>();
+  constexpr int NT = G >= 8 ? 768 : 256;
+  constexpr int GPB = NT / G;
+  const int64_t gx = (a.Dm + GPB - 1) / GPB;
+  if (gx > 0x7fffffffLL || a.batch > 65535) return MQC_E_LIMIT;
+  const dim3 grid((unsigned)gx, (unsigned)a.batch);
+  if (a.S == G)
+    ssm_bwd_kernel<T, G, K, NT, true><<<grid, dim3(NT), 0, s>>>(a);
+  else
+    ssm_bwd_kernel<T, G, K, NT, false><<<grid, dim3(NT), 0, s>>>(a);
+  return launch_status();
+}
+
+template <typename T>
+int launch_ssm_bwd(const SsmBwdArgs& a, hipStream_t s) {
+  if (a.batch == 0 || a.T == 0 || a.Dm == 0) return MQC_OK;
+  if (a.Dm * a.S * 4 * (int64_t)sizeof(T) >= ((int64_t)1 << 31)) return MQC_E_LIMIT;
+  const uintptr_t qa = 4 * sizeof(T);
+  if (!aligned(a.Bm, qa) || !aligned(a.Cm, qa) || !aligned(a.gy, qa) || !aligned(a.dB, qa) ||
+      !aligned(a.dC, qa) || !aligned(a.h_ckpt, 16) || (a.h0 && !aligned(a.h0, qa)) ||
+      (a.dh_last && !aligned(a.dh_last, qa)) || (a.dh0 && !aligned(a.dh0, qa)) ||
+      !aligned(a.delta, sizeof(T)) || !aligned(a.s, sizeof(T)) || !aligned(a.d_delta, 4) ||
+      !aligned(a.d_s, 4))
+    return MQC_E_ALIGN;
+  const int64_t S = a.S;
+  if (S <= 1) return launch_ssm_bwd_g<T, 1>(a, s);
+  if (S <= 2) return launch_ssm_bwd_g<T, 2>(a, s);
+  if (S <= 4) return launch_ssm_bwd_g<T, 4>(a, s);
+  if (S <= 8) return launch_ssm_bwd_g<T, 8>(a, s);
+  if (S <= 16) return launch_ssm_bwd_g<T, 16>(a, s);
+  if (S <= 32) return launch_ssm_bwd_g<T, 32>(a, s);
+  if (S <= 64) return launch_ssm_bwd_g<T, 64>(a, s);
+  return MQC_E_LIMIT;
+}
+
+extern template int launch_ssm_bwd<float>(const SsmBwdArgs&, hipStream_t);
+extern template int launch_ssm_bwd<bf16_t>(const SsmBwdArgs&, hipStream_t);
+extern template int launch_ssm_bwd<f16_t>(const SsmBwdArgs&, hipStream_t);
+
+}  // namespace mqc

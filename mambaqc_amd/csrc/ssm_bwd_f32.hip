@@ -1,0 +1,6 @@
+// Instantiation of the fused quaternion SSM backward for f32 storage (ssm_bwd.hpp).
+#include "ssm_bwd.hpp"
+
+namespace mqc {
+template int launch_ssm_bwd<float>(const SsmBwdArgs&, hipStream_t);
+}  // namespace mqc

@@ -126,6 +126,10 @@ struct SsmArgs {
   const void* h0;
   void* y;
   void* h_last;
+  // Optional fp32 state checkpoints [B, ceil(T/ckpt_every), D, S, 4]: the state
+  // at the last step of every chunk of ckpt_every steps (for the backward).
+  float* h_ckpt;
+  int64_t ckpt_every;
   int64_t batch, T, Dm, S;
   float eps;
 };
@@ -199,6 +203,40 @@ __device__ inline float softplus_f(float x) {
   return x > 20.f ? x : log1pf(expf(x));
 }
 
+// Per-(d,k) constants of the Cayley closed form for Lambda = (a, v):
+// a = -softplus(alpha), v = tanh(imag), n2 = |Lambda|^2 / 4.
+struct LamConst {
+  float a, n2, v0, v1, v2;
+};
+
+__device__ inline LamConst lam_const(const float* lam_alpha, const float* lam_imag, int64_t dk) {
+  LamConst c;
+  c.a = -softplus_f(lam_alpha[dk]);
+  c.v0 = tanhf(lam_imag[dk * 3 + 0]);
+  c.v1 = tanhf(lam_imag[dk * 3 + 1]);
+  c.v2 = tanhf(lam_imag[dk * 3 + 2]);
+  c.n2 = 0.25f * (c.a * c.a + c.v0 * c.v0 + c.v1 * c.v1 + c.v2 * c.v2);
+  return c;
+}
+
+// q = Cayley(dl * Lambda) = ((1 - dl^2 n2) / N, dl v / N), N = max(1 - dl a + dl^2 n2, eps).
+// The forward kernel and the backward's recompute share this code, so both
+// produce the same q.
+__device__ inline quat cayley_step(float dl, float dl2, const LamConst& L, float eps) {
+  float N = fmaf(dl2, L.n2, fmaf(-dl, L.a, 1.f));
+  N = fmaxf(N, eps);
+  const float r = __builtin_amdgcn_rcpf(N);
+  const float c = dl * r;
+  return quat{fmaf(-dl2, L.n2, 1.f) * r, c * L.v0, c * L.v1, c * L.v2};
+}
+
+// h_t = q (x) h_{t-1} + s * B
+__device__ inline quat state_step(const quat& q, const quat& h, float sv, const quat& Bk) {
+  quat hn{sv * Bk.w, sv * Bk.x, sv * Bk.y, sv * Bk.z};
+  qmul_acc(hn, q, h);
+  return hn;
+}
+
 // FULL: S == KPL * G, so every lane of a group owns real states.
 // SYNC: 0 = waves run freely; 1 = block barrier after every step; 2 = after
 // every PF steps.
@@ -228,20 +266,11 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   const uint32_t offQ4 = (uint32_t)(d * 4 * (int64_t)sizeof(T));
 
   // Per-(d,k) constants of the Cayley closed form (MODE_DL).
-  float la[KPL], ln2[KPL], lv[KPL][3];
+  LamConst lam[KPL];
   float dskip = 0.f;
   if constexpr (MODE == MODE_DL) {
 #pragma unroll
-    for (int kk = 0; kk < KPL; ++kk) {
-      const int64_t dk = d * a.S + k0 + kk;
-      const float ar = -softplus_f(a.lam_alpha[dk]);
-      const float v0 = tanhf(a.lam_imag[dk * 3 + 0]);
-      const float v1 = tanhf(a.lam_imag[dk * 3 + 1]);
-      const float v2 = tanhf(a.lam_imag[dk * 3 + 2]);
-      la[kk] = ar;
-      ln2[kk] = 0.25f * (ar * ar + v0 * v0 + v1 * v1 + v2 * v2);
-      lv[kk][0] = v0; lv[kk][1] = v1; lv[kk][2] = v2;
-    }
+    for (int kk = 0; kk < KPL; ++kk) lam[kk] = lam_const(a.lam_alpha, a.lam_imag, d * a.S + k0 + kk);
     dskip = a.dvec[d];
   }
 
@@ -279,6 +308,10 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
 
   const bool writer = gvalid && (G < 4 || j < 4);
   const int64_t rowY = a.Dm * 4;
+  // Checkpoint schedule (scalar): the next step whose state is saved.
+  const int64_t n_ckpt = a.h_ckpt ? (Tn + a.ckpt_every - 1) / a.ckpt_every : 0;
+  int64_t next_ckpt = a.h_ckpt ? (a.ckpt_every < Tn ? a.ckpt_every - 1 : Tn - 1) : -1;
+  int64_t ckpt_idx = 0;
 
   for (int64_t t0 = 0; t0 < Tn; t0 += PF) {
 #pragma unroll
@@ -297,17 +330,9 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
         const float dl2 = dl * dl;
 #pragma unroll
         for (int kk = 0; kk < KPL; ++kk) {
-          float N = fmaf(dl2, ln2[kk], fmaf(-dl, la[kk], 1.f));
-          N = fmaxf(N, a.eps);
-          const float r = __builtin_amdgcn_rcpf(N);
-          const float c = dl * r;
-          const quat qd{fmaf(-dl2, ln2[kk], 1.f) * r, c * lv[kk][0], c * lv[kk][1],
-                        c * lv[kk][2]};
-          const quat Bk = raw_quat(cur.B, kk);
-          quat hn{sv * Bk.w, sv * Bk.x, sv * Bk.y, sv * Bk.z};
-          qmul_acc(hn, qd, h[kk]);
-          h[kk] = hn;
-          qmul_acc(acc, raw_quat(cur.C, kk), hn);
+          const quat qd = cayley_step(dl, dl2, lam[kk], a.eps);
+          h[kk] = state_step(qd, h[kk], sv, raw_quat(cur.B, kk));
+          qmul_acc(acc, raw_quat(cur.C, kk), h[kk]);
         }
       } else {
         const quat Sq = raw_quat(cur.S, 0);
@@ -347,6 +372,20 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (e < nc) store_scalar(yo + c0 + e, v[e]);
+      }
+      if (a.h_ckpt && t == next_ckpt) {
+        // Chunk t / ckpt_every ends here (or the sequence does).
+        if (gvalid && kvalid) {
+          float e[4 * KPL];
+#pragma unroll
+          for (int kk = 0; kk < KPL; ++kk) {
+            e[4 * kk + 0] = h[kk].w; e[4 * kk + 1] = h[kk].x;
+            e[4 * kk + 2] = h[kk].y; e[4 * kk + 3] = h[kk].z;
+          }
+          store_vec<float, 4 * KPL>(a.h_ckpt + (((b * n_ckpt + ckpt_idx) * a.Dm + d) * a.S + k0) * 4, e);
+        }
+        ++ckpt_idx;
+        next_ckpt = next_ckpt + a.ckpt_every < Tn ? next_ckpt + a.ckpt_every : Tn - 1;
       }
       if constexpr (SYNC == 1) __syncthreads();
     }

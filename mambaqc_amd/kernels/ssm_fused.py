@@ -92,6 +92,88 @@ def ssm_forward_fused(q: torch.Tensor, B: torch.Tensor, S: torch.Tensor, C: torc
     return y
 
 
+def _dl_check(delta, s, B, C, lambda_alpha, lambda_imag, D, h0):
+    batch, T, d_inner, d_state, four = B.shape
+    assert four == 4
+    assert C.shape == B.shape
+    assert delta.shape == (batch, T, d_inner) and s.shape == (batch, T, d_inner)
+    assert lambda_alpha.shape == (d_inner, d_state)
+    assert lambda_imag.shape == (d_inner, d_state, 3)
+    assert D.shape == (d_inner,)
+    if h0 is not None:
+        assert h0.shape == (batch, d_inner, d_state, 4)
+    nat.require_device("ssm_forward_fused_dl", delta, s, B, C, lambda_alpha, lambda_imag, D)
+    if C.dtype != B.dtype:
+        raise TypeError(f"ssm_forward_fused_dl: dtype mismatch {B.dtype} vs {C.dtype}")
+    return batch, T, d_inner, d_state
+
+
+def _dl_operands(delta, s, B, C, lambda_alpha, lambda_imag, D, h0):
+    """Contiguous, aligned operands in the kernel's types (fp32 parameters)."""
+    dtype = B.dtype
+    ops = [nat.aligned16(t.detach().to(dtype)) for t in (delta, s)]
+    ops += [nat.aligned16(t.detach()) for t in (B, C)]
+    ops += [nat.aligned16(t.detach().float()) for t in (lambda_alpha, lambda_imag, D)]
+    ops.append(None if h0 is None else nat.aligned16(h0.detach().to(dtype)))
+    return ops
+
+
+class _SsmFusedDL(torch.autograd.Function):
+    """Autograd wrapper: training forward (state checkpoints) + HIP backward."""
+
+    @staticmethod
+    def forward(ctx, delta, s, B, C, lambda_alpha, lambda_imag, D, h0, eps):
+        batch, T, d_inner, d_state = _dl_check(delta, s, B, C, lambda_alpha, lambda_imag, D, h0)
+        dl, sv, Bc, Cc, la, li, Dv, h0c = _dl_operands(delta, s, B, C, lambda_alpha,
+                                                       lambda_imag, D, h0)
+        dtype = Bc.dtype
+        code = nat.dtype_code(Bc)
+        K = nat.load().mqc_ssm_bwd_ckpt_every(code)
+        n_ckpt = (T + K - 1) // K
+        y = torch.empty(batch, T, d_inner, 4, device=Bc.device, dtype=dtype)
+        h_last = torch.empty(batch, d_inner, d_state, 4, device=Bc.device, dtype=dtype)
+        ckpt = torch.empty(batch, max(n_ckpt, 1), d_inner, d_state, 4, device=Bc.device,
+                           dtype=torch.float32)
+        nat.call("mqc_ssm_fused_fwd_train", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
+                 Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
+                 y.data_ptr(), h_last.data_ptr(), ckpt.data_ptr(), K, batch, T, d_inner,
+                 d_state, float(eps), code, nat.stream_of(Bc))
+        ctx.save_for_backward(dl, sv, Bc, Cc, la, li, Dv, h0c, ckpt)
+        ctx.meta = (eps, K, delta.dtype, s.dtype, lambda_alpha.dtype, lambda_imag.dtype,
+                    D.dtype, None if h0 is None else h0.dtype)
+        return y, h_last
+
+    @staticmethod
+    def backward(ctx, gy, gh_last):
+        dl, sv, Bc, Cc, la, li, Dv, h0c, ckpt = ctx.saved_tensors
+        eps, K, t_delta, t_s, t_la, t_li, t_D, t_h0 = ctx.meta
+        batch, T, d_inner, d_state, _ = Bc.shape
+        dtype = Bc.dtype
+        dev = Bc.device
+        if gy is None:
+            gy = torch.zeros(batch, T, d_inner, 4, device=dev, dtype=dtype)
+        gy = nat.aligned16(gy.to(dtype))
+        if gh_last is not None:
+            gh_last = nat.aligned16(gh_last.to(dtype))
+        d_delta = torch.empty(dl.shape, device=dev, dtype=torch.float32)
+        d_s = torch.empty(sv.shape, device=dev, dtype=torch.float32)
+        dB = torch.empty_like(Bc)
+        dC = torch.empty_like(Cc)
+        dla = torch.empty(batch, d_inner, d_state, device=dev, dtype=torch.float32)
+        dli = torch.empty(batch, d_inner, d_state, 3, device=dev, dtype=torch.float32)
+        dD = torch.empty(batch, d_inner, device=dev, dtype=torch.float32)
+        dh0 = torch.empty_like(h0c) if h0c is not None else None
+        nat.call("mqc_ssm_fused_bwd", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
+                 Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
+                 ckpt.data_ptr(), K, gy.data_ptr(), nat.ptr(gh_last), d_delta.data_ptr(),
+                 d_s.data_ptr(), dB.data_ptr(), dC.data_ptr(), dla.data_ptr(), dli.data_ptr(),
+                 dD.data_ptr(), nat.ptr(dh0), batch, T, d_inner, d_state, float(eps),
+                 nat.dtype_code(Bc), nat.stream_of(Bc))
+        return (d_delta.to(t_delta), d_s.to(t_s), dB, dC, dla.sum(0).to(t_la),
+                dli.sum(0).to(t_li), dD.sum(0).to(t_D),
+                None if dh0 is None else dh0.to(t_h0), None)
+
+
 def ssm_forward_fused_dl(delta: torch.Tensor, s: torch.Tensor, B: torch.Tensor,
                          C: torch.Tensor, lambda_alpha: torch.Tensor,
                          lambda_imag: torch.Tensor, D: torch.Tensor, eps: float = 1e-6,
@@ -104,34 +186,22 @@ def ssm_forward_fused_dl(delta: torch.Tensor, s: torch.Tensor, B: torch.Tensor,
     Computes Lambda = (-softplus(lambda_alpha), tanh(lambda_imag)),
     q_t = Cayley(delta_t * Lambda, eps), and the recurrence with S = (s, 0, 0, 0).
     Returns y [batch, seq_len, d_inner, 4] in B's dtype (and the final state if
-    return_state).
+    return_state). Differentiable in every tensor argument when autograd is
+    recording (HIP backward, d_state <= 64); otherwise a single inference launch.
     """
-    batch, T, d_inner, d_state, four = B.shape
-    assert four == 4
-    assert C.shape == B.shape
-    assert delta.shape == (batch, T, d_inner) and s.shape == (batch, T, d_inner)
-    assert lambda_alpha.shape == (d_inner, d_state)
-    assert lambda_imag.shape == (d_inner, d_state, 3)
-    assert D.shape == (d_inner,)
-    nat.require_device("ssm_forward_fused_dl", delta, s, B, C, lambda_alpha, lambda_imag, D)
-    dtype = B.dtype
-    if C.dtype != dtype:
-        raise TypeError(f"ssm_forward_fused_dl: dtype mismatch {dtype} vs {C.dtype}")
-    delta = nat.aligned16(delta.to(dtype))
-    s = nat.aligned16(s.to(dtype))
-    B = nat.aligned16(B)
-    C = nat.aligned16(C)
-    la = nat.aligned16(lambda_alpha.detach().float())
-    li = nat.aligned16(lambda_imag.detach().float())
-    Dv = nat.aligned16(D.detach().float())
-    y = torch.empty(batch, T, d_inner, 4, device=B.device, dtype=dtype)
-    h_last = (torch.empty(batch, d_inner, d_state, 4, device=B.device, dtype=dtype)
+    inputs = (delta, s, B, C, lambda_alpha, lambda_imag, D) + ((h0,) if h0 is not None else ())
+    if torch.is_grad_enabled() and any(t.requires_grad for t in inputs):
+        y, h_last = _SsmFusedDL.apply(delta, s, B, C, lambda_alpha, lambda_imag, D, h0, eps)
+        return (y, h_last) if return_state else y
+    batch, T, d_inner, d_state = _dl_check(delta, s, B, C, lambda_alpha, lambda_imag, D, h0)
+    dl, sv, Bc, Cc, la, li, Dv, h0c = _dl_operands(delta, s, B, C, lambda_alpha, lambda_imag,
+                                                   D, h0)
+    dtype = Bc.dtype
+    y = torch.empty(batch, T, d_inner, 4, device=Bc.device, dtype=dtype)
+    h_last = (torch.empty(batch, d_inner, d_state, 4, device=Bc.device, dtype=dtype)
               if return_state else None)
-    if h0 is not None:
-        assert h0.shape == (batch, d_inner, d_state, 4)
-        h0 = nat.aligned16(h0.to(dtype))
-    nat.call("mqc_ssm_fused_fwd", B, delta.data_ptr(), s.data_ptr(), B.data_ptr(),
-             C.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0),
+    nat.call("mqc_ssm_fused_fwd", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
+             Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
              y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state, float(eps),
-             nat.dtype_code(B), nat.stream_of(B))
+             nat.dtype_code(Bc), nat.stream_of(Bc))
     return (y, h_last) if return_state else y

@@ -14,8 +14,12 @@ from .quat import qln_reference, ssm_forward_dl_reference
 
 def block_forward_reference(sd: dict, x: torch.Tensor, d_state: int, d_conv: int = 4,
                             eps_cayley: float = 1e-6, eps_norm: float = 1e-5) -> torch.Tensor:
-    """x: [b, T, d_model] (CPU) -> [b, T, d_model]."""
-    sd = {k: v.detach().cpu().to(x.dtype) for k, v in sd.items()}
+    """x: [b, T, d_model] (CPU) -> [b, T, d_model].
+
+    Differentiable in x and in every state-dict entry that requires grad (the
+    backward's oracle is torch autograd through this function).
+    """
+    sd = {k: v.cpu().to(x.dtype) for k, v in sd.items()}
     b, T, d_model = x.shape
     # in_proj + chunk (:137-138)
     xz = F.linear(x, sd["in_proj.weight"], sd.get("in_proj.bias"))

@@ -29,7 +29,7 @@ def declared_symbols():
 
 def test_header_declares_the_api():
     names = declared_symbols()
-    assert len(names) == 12, names
+    assert len(names) == 17, names
     assert set(nat.SIGNATURES) <= set(names)
 
 
@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     lib = nat.load()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mqc_abi_version() == 1
+    assert lib.mqc_abi_version() == nat.ABI_VERSION == 2
 
 
 def test_status_strings():
@@ -97,10 +97,36 @@ def test_wrappers_refuse_cpu_tensors():
         K.QuaternionLayerNorm(3)(torch.zeros(1, 2, 3, 4))
 
 
-def test_block_refuses_grad_until_backward_exists():
+def test_block_training_forward_refuses_cpu():
     blk = mambaqc_amd.QuaternionMamba2Block(8, d_state=2)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="ROCm device"):
         blk(torch.zeros(1, 3, 8))
+
+
+def test_training_validation_codes_without_gpu():
+    lib = nat.load()
+    assert lib.mqc_ssm_bwd_ckpt_every(0) == 4
+    assert lib.mqc_ssm_bwd_ckpt_every(1) == 8
+    assert lib.mqc_ssm_bwd_ckpt_every(2) == 8
+    assert lib.mqc_ssm_bwd_ckpt_every(5) == -3
+    P = [FAKE] * 7
+    # Checkpoint interval below 1.
+    assert lib.mqc_ssm_fused_fwd_train(*P, None, FAKE, None, FAKE, 0, 1, 4, 2, 8,
+                                       1e-6, 1, None) == -2
+    # Missing checkpoint buffer.
+    assert lib.mqc_ssm_fused_fwd_train(*P, None, FAKE, None, None, 8, 1, 4, 2, 8,
+                                       1e-6, 1, None) == -1
+    # Backward: interval other than the one the kernel needs, then d_state > 64.
+    G = [FAKE] * 7
+    assert lib.mqc_ssm_fused_bwd(*P, None, FAKE, 5, FAKE, None, *G, None, 1, 4, 2, 8,
+                                 1e-6, 1, None) == -5
+    assert lib.mqc_ssm_fused_bwd(*P, None, FAKE, 8, FAKE, None, *G, None, 1, 4, 2, 65,
+                                 1e-6, 1, None) == -5
+    # QLN backward: empty rows are an error, nothing to do is not.
+    assert lib.mqc_qln_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 3, 0, 1e-5, 0, None) == -2
+    assert lib.mqc_qln_bwd(None, None, None, None, None, None, None, 0, 4, 1e-5, 0, None) == 0
+    # Gate backward: dz narrower than the gated columns.
+    assert lib.mqc_out_gate_bwd(FAKE, FAKE, 8, FAKE, FAKE, FAKE, 2, 8, 4, 0, None) == -2
 
 
 def test_block_seeded_init_matches_reference():
