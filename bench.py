@@ -1,6 +1,6 @@
 """Benchmark: QuaternionMamba2Block forward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--mode full|ssm|cumprod|qln|copy]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--mode full|ssm|ssm_bwd|cumprod|cayley|qln|copy]
 
 Workload (BASELINE configs[2]/[3] shape): one QuaternionMamba2Block forward,
 batch 4, seq_len 2048, d_model 768, d_state 64, d_conv 4, expand_factor 2
@@ -12,7 +12,10 @@ timed region bracketed by torch.cuda.synchronize()). `roofline` is the fused
 SSM kernel (mqc_ssm_fused_fwd): algorithmic bytes per launch divided by its
 mean launch duration, measured with HIP events on the stream it runs on.
 `cpu_baseline` times the CPU oracle (a restatement of the reference's
-sequential torch path) on a bounded prefix of the same workload.
+sequential torch path) on a bounded prefix of the same workload. `train_c4`
+reports config 4 (block forward + backward under fp16 autocast) and the SSM's
+training-forward and backward kernels at the same shape; `lm_c5` the base
+preset LM forward (config 5).
 
 The other modes run one kernel in a loop for rocprofv3 (no JSON contract).
 """
@@ -45,6 +48,17 @@ def ssm_bytes(b, t, d, s, el=2):
 
 def qln_bytes(rows, d, el=2):
     return 2 * rows * d * 4 * el + d * 4 + d * 16
+
+
+def ssm_bwd_bytes(b, t, d, s, el=2, ckpt_every=8):
+    """Algorithmic HBM bytes of one SSM backward launch: reads delta, s, B, C,
+    gy (storage dtype), the fp32 state checkpoints and Lambda/D; writes dB, dC
+    (storage dtype), d_delta, d_s (fp32) and the per-batch parameter partials."""
+    n_ckpt = -(-t // ckpt_every)
+    reads = (2 * b * t * d * el + 2 * b * t * d * s * 4 * el + b * t * d * 4 * el
+             + b * n_ckpt * d * s * 4 * 4 + d * s * 4 * 4 + d * 4)
+    writes = 2 * b * t * d * s * 4 * el + 2 * b * t * d * 4 + b * d * s * 4 * 4 + b * d * 4
+    return reads + writes
 
 
 def log(msg):
@@ -204,6 +218,9 @@ def run_full(args):
     del z, q
     torch.cuda.empty_cache()
 
+    train = train_timings(args)
+    lm = lm_timing(args)
+
     base = None if args.no_cpu else cpu_baseline(blk, x)
     if base:
         log(f"cpu baseline: {base['value']} tokens/s on {base['cores']} threads")
@@ -245,9 +262,103 @@ def run_full(args):
             "cayley_c2_ms": round(cay_ms, 4),
             "cumprod_scan_c2_ms": round(scan_ms, 4),
         },
+        "train_c4": train,
+        "lm_c5": lm,
         "cpu_baseline": base,
     }
     print(json.dumps(result), flush=True)
+
+
+def train_timings(args):
+    """Config 4: block forward + backward under fp16 autocast (loss scaled as
+    GradScaler does), and the SSM's training forward and backward kernels alone
+    at the same shape (bf16 storage)."""
+    import torch
+    from mambaqc_amd.kernels.ssm_fused import ssm_fused_dl_backward, ssm_fused_dl_train_forward
+
+    torch.manual_seed(0)
+    blk = make_block(torch.float32)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(B, T, DM, generator=g, device="cuda")
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = blk(x).float().pow(2).mean()
+        (loss * 2.0 ** 16).backward()
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    reps = max(3, min(args.steps, 10))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    log(f"config 4 block fwd+bwd (fp16 autocast): {ms:.2f} ms/step, {B * T / ms * 1e3:.0f} tokens/s")
+    del blk
+    torch.cuda.empty_cache()
+
+    bf = torch.bfloat16
+    delta = torch.nn.functional.softplus(torch.randn(B, T, DI, generator=g, device="cuda") - 2).to(bf)
+    s = torch.randn(B, T, DI, generator=g, device="cuda").to(bf)
+    Bq = torch.randn(B, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
+    Cq = torch.randn(B, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
+    la = torch.randn(DI, DS, generator=g, device="cuda") * 0.5 + 1
+    li = torch.randn(DI, DS, 3, generator=g, device="cuda") * 0.1
+    Dv = torch.ones(DI, device="cuda")
+    gy = torch.randn(B, T, DI, 4, generator=g, device="cuda").to(bf)
+    with torch.no_grad():
+        _, _, saved = ssm_fused_dl_train_forward(delta, s, Bq, Cq, la, li, Dv)
+        fwd_ms = event_time_ms(lambda: ssm_fused_dl_train_forward(delta, s, Bq, Cq, la, li, Dv), 5)
+        ssm_fused_dl_backward(saved, gy)
+        bwd_ms = event_time_ms(lambda: ssm_fused_dl_backward(saved, gy), 5)
+    n_ckpt = -(-T // 8)
+    fwd_bytes = ssm_bytes(B, T, DI, DS) + B * n_ckpt * DI * DS * 16
+    bwd_bytes = ssm_bwd_bytes(B, T, DI, DS)
+    log(f"ssm train fwd {fwd_ms:.3f} ms ({fwd_bytes / fwd_ms / 1e6:.0f} GB/s), "
+        f"bwd {bwd_ms:.3f} ms ({bwd_bytes / bwd_ms / 1e6:.0f} GB/s)")
+    return {
+        "workload": "QuaternionMamba2Block forward+backward, fp16 autocast, B4 T2048 d768 s64",
+        "ms_per_step": round(ms, 3),
+        "tokens_per_s": round(B * T / ms * 1e3, 1),
+        "ssm_train_fwd_ms": round(fwd_ms, 4),
+        "ssm_train_fwd_GBs": round(fwd_bytes / fwd_ms / 1e6, 1),
+        "ssm_bwd_ms": round(bwd_ms, 4),
+        "ssm_bwd_GBs": round(bwd_bytes / bwd_ms / 1e6, 1),
+        "ssm_bwd_algorithmic_bytes": bwd_bytes,
+    }
+
+
+def lm_timing(args):
+    """Config 5: the 12-layer base preset (14.66 B parameters) forward in bf16 at
+    B4 T2048, vocab 10000, input ids uniform in [0, 10000), random-init weights."""
+    import torch
+    import mambaqc_amd
+
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        lm = mambaqc_amd.quaternion_mamba2_base(10000)
+    lm = lm.to(torch.bfloat16).eval()
+    g = torch.Generator(device="cuda").manual_seed(0)
+    ids = torch.randint(0, 10000, (B, T), generator=g, device="cuda")
+    reps = max(2, min(args.steps, 5))
+    with torch.inference_mode():
+        lm(ids)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            lm(ids)
+        torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    n_params = sum(p.numel() for p in lm.parameters())
+    log(f"config 5 LM forward ({n_params / 1e9:.2f} B params, bf16): {ms:.1f} ms, "
+        f"{B * T / ms * 1e3:.0f} tokens/s")
+    del lm
+    torch.cuda.empty_cache()
+    return {"workload": "QuaternionMamba2 base (12 layers) forward, bf16, B4 T2048, vocab 10000",
+            "params": n_params, "ms_per_step": round(ms, 2),
+            "tokens_per_s": round(B * T / ms * 1e3, 1)}
 
 
 def run_kernel_loop(args):
@@ -269,6 +380,21 @@ def run_kernel_loop(args):
             Dv = torch.ones(DI, device="cuda")
             fn = lambda: K.ssm_forward_fused_dl(delta, s, Bq, Cq, la, li, Dv)
             nbytes = ssm_bytes(B, T, DI, DS)
+        elif args.mode == "ssm_bwd":
+            from mambaqc_amd.kernels.ssm_fused import (ssm_fused_dl_backward,
+                                                       ssm_fused_dl_train_forward)
+            bf = torch.bfloat16
+            delta = torch.nn.functional.softplus(torch.randn(B, T, DI, generator=g, device="cuda") - 2).to(bf)
+            s = torch.randn(B, T, DI, generator=g, device="cuda").to(bf)
+            Bq = torch.randn(B, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
+            Cq = torch.randn(B, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
+            la = torch.randn(DI, DS, generator=g, device="cuda") * 0.5 + 1
+            li = torch.randn(DI, DS, 3, generator=g, device="cuda") * 0.1
+            Dv = torch.ones(DI, device="cuda")
+            gy = torch.randn(B, T, DI, 4, generator=g, device="cuda").to(bf)
+            _, _, saved = ssm_fused_dl_train_forward(delta, s, Bq, Cq, la, li, Dv)
+            fn = lambda: ssm_fused_dl_backward(saved, gy)
+            nbytes = ssm_bwd_bytes(B, T, DI, DS)
         elif args.mode in ("cumprod", "cayley"):
             q = torch.randn(2, 256, 768, 64, 4, generator=g, device="cuda")
             q = q / q.norm(dim=-1, keepdim=True)

@@ -5,12 +5,25 @@ Drop-in for the reference package's hot path (polux06/mambaqc):
                         quaternion_multiply (+ conjugate/inverse/norm),
                         ssm_step_fused, ssm_forward_fused, quaternion_layer_norm_fused
   mambaqc_amd.layers    QuaternionLinear, QuaternionLayerNorm, CausalConv1d
-  mambaqc_amd           QuaternionMamba2Block
-All compute runs in libmambaqc_hip.so (hand-written HIP, C ABI in
-include/mambaqc_hip.h); there is no CPU fallback.
+  mambaqc_amd           QuaternionMamba2Block, QuaternionMamba2 (+ presets)
+All compute of the quaternion path runs in libmambaqc_hip.so (hand-written
+HIP, C ABI in include/mambaqc_hip.h); there is no CPU fallback.
 """
 __version__ = "0.1.0"
 
 from .block import QuaternionMamba2Block, out_gate
+from .lm import (
+    QuaternionMamba2,
+    quaternion_mamba2_base,
+    quaternion_mamba2_large,
+    quaternion_mamba2_small,
+)
 
-__all__ = ["QuaternionMamba2Block", "out_gate"]
+__all__ = [
+    "QuaternionMamba2",
+    "QuaternionMamba2Block",
+    "out_gate",
+    "quaternion_mamba2_small",
+    "quaternion_mamba2_base",
+    "quaternion_mamba2_large",
+]

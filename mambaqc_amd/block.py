@@ -149,7 +149,32 @@ class QuaternionMamba2Block(nn.Module):
         y_real = self.out_proj(y)
         return out_gate(x, z, y_real)
 
-    def _ssm_forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward_with_state(self, x: torch.Tensor, state=None):
+        """forward() continued from a recurrent state; returns (out, new_state).
+
+        state = (conv_tail, h): conv_tail [batch, d_conv - 1, d_inner] holds the
+        last d_conv - 1 conv inputs, h [batch, d_inner, d_state, 4] the SSM
+        state. None starts from zeros, where the result equals forward(x).
+        Feeding a sequence in pieces gives the same outputs as feeding it whole
+        (up to rounding), which is what recurrent decoding relies on.
+        """
+        xz = self.in_proj(x)
+        x_in, z = xz.chunk(2, dim=-1)
+        b, _, D = x_in.shape
+        k = self.d_conv - 1
+        if state is None:
+            tail, h0 = x_in.new_zeros(b, k, D), None
+        else:
+            tail, h0 = state
+        xc = torch.cat([tail.to(x_in.dtype), x_in], dim=1)
+        conv = self.conv1d.conv
+        x_act = F.silu(F.conv1d(xc.transpose(1, 2), conv.weight, conv.bias, groups=D).transpose(1, 2))
+        y, h = self._ssm_forward(x_act, h0=h0, return_state=True)
+        y_real = self.out_proj(self.norm(y))
+        return out_gate(x, z, y_real), (xc[:, xc.shape[1] - k:], h)
+
+    def _ssm_forward(self, x: torch.Tensor, h0: torch.Tensor | None = None,
+                     return_state: bool = False):
         """x: [batch, seq_len, d_inner] (real) -> y: [batch, seq_len, d_inner, 4]."""
         b, t, D = x.shape
         delta = F.softplus(self.dt_proj(x))
@@ -157,7 +182,7 @@ class QuaternionMamba2Block(nn.Module):
         Cq = self.C_proj(x).view(b, t, D, self.d_state, 4)
         s = torch.sigmoid(self.gate_proj(x)) * x
         return ssm_forward_fused_dl(delta, s, Bq, Cq, self.Lambda_alpha, self.Lambda_imag,
-                                    self.D, eps=1e-6)
+                                    self.D, eps=1e-6, h0=h0, return_state=return_state)
 
     def extra_repr(self) -> str:
         return (f"d_model={self.d_model}, d_state={self.d_state}, d_inner={self.d_inner}, "

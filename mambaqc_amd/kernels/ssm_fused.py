@@ -118,60 +118,86 @@ def _dl_operands(delta, s, B, C, lambda_alpha, lambda_imag, D, h0):
     return ops
 
 
+def ssm_fused_dl_train_forward(delta, s, B, C, lambda_alpha, lambda_imag, D, h0=None,
+                               eps: float = 1e-6):
+    """Training forward of the block's SSM: y, the final state, and what the
+    backward needs (the kernel operands and the fp32 state checkpoints).
+
+    Returns (y, h_last, saved) with saved = (delta, s, B, C, lambda_alpha,
+    lambda_imag, D, h0, checkpoints) in the kernel's types.
+    """
+    batch, T, d_inner, d_state = _dl_check(delta, s, B, C, lambda_alpha, lambda_imag, D, h0)
+    dl, sv, Bc, Cc, la, li, Dv, h0c = _dl_operands(delta, s, B, C, lambda_alpha, lambda_imag,
+                                                   D, h0)
+    code = nat.dtype_code(Bc)
+    K = nat.load().mqc_ssm_bwd_ckpt_every(code)
+    n_ckpt = (T + K - 1) // K
+    y = torch.empty(batch, T, d_inner, 4, device=Bc.device, dtype=Bc.dtype)
+    h_last = torch.empty(batch, d_inner, d_state, 4, device=Bc.device, dtype=Bc.dtype)
+    ckpt = torch.empty(batch, max(n_ckpt, 1), d_inner, d_state, 4, device=Bc.device,
+                       dtype=torch.float32)
+    nat.call("mqc_ssm_fused_fwd_train", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
+             Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
+             y.data_ptr(), h_last.data_ptr(), ckpt.data_ptr(), K, batch, T, d_inner, d_state,
+             float(eps), code, nat.stream_of(Bc))
+    return y, h_last, (dl, sv, Bc, Cc, la, li, Dv, h0c, ckpt)
+
+
+def ssm_fused_dl_backward(saved, gy, gh_last=None, eps: float = 1e-6):
+    """Backward of ssm_fused_dl_train_forward given dL/dy (and dL/dh_last).
+
+    Returns (d_delta, d_s fp32 [batch, T, d_inner], dB, dC in B's dtype,
+    dlambda_alpha, dlambda_imag, dD fp32 (summed over the batch), dh0 or None).
+    """
+    dl, sv, Bc, Cc, la, li, Dv, h0c, ckpt = saved
+    batch, T, d_inner, d_state, _ = Bc.shape
+    dtype, dev = Bc.dtype, Bc.device
+    code = nat.dtype_code(Bc)
+    K = nat.load().mqc_ssm_bwd_ckpt_every(code)
+    if gy is None:
+        gy = torch.zeros(batch, T, d_inner, 4, device=dev, dtype=dtype)
+    gy = nat.aligned16(gy.to(dtype))
+    if gh_last is not None:
+        gh_last = nat.aligned16(gh_last.to(dtype))
+    d_delta = torch.empty(dl.shape, device=dev, dtype=torch.float32)
+    d_s = torch.empty(sv.shape, device=dev, dtype=torch.float32)
+    dB = torch.empty_like(Bc)
+    dC = torch.empty_like(Cc)
+    dla = torch.empty(batch, d_inner, d_state, device=dev, dtype=torch.float32)
+    dli = torch.empty(batch, d_inner, d_state, 3, device=dev, dtype=torch.float32)
+    dD = torch.empty(batch, d_inner, device=dev, dtype=torch.float32)
+    dh0 = torch.empty_like(h0c) if h0c is not None else None
+    nat.call("mqc_ssm_fused_bwd", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
+             Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
+             ckpt.data_ptr(), K, gy.data_ptr(), nat.ptr(gh_last), d_delta.data_ptr(),
+             d_s.data_ptr(), dB.data_ptr(), dC.data_ptr(), dla.data_ptr(), dli.data_ptr(),
+             dD.data_ptr(), nat.ptr(dh0), batch, T, d_inner, d_state, float(eps), code,
+             nat.stream_of(Bc))
+    return d_delta, d_s, dB, dC, dla.sum(0), dli.sum(0), dD.sum(0), dh0
+
+
 class _SsmFusedDL(torch.autograd.Function):
     """Autograd wrapper: training forward (state checkpoints) + HIP backward."""
 
     @staticmethod
     def forward(ctx, delta, s, B, C, lambda_alpha, lambda_imag, D, h0, eps):
-        batch, T, d_inner, d_state = _dl_check(delta, s, B, C, lambda_alpha, lambda_imag, D, h0)
-        dl, sv, Bc, Cc, la, li, Dv, h0c = _dl_operands(delta, s, B, C, lambda_alpha,
-                                                       lambda_imag, D, h0)
-        dtype = Bc.dtype
-        code = nat.dtype_code(Bc)
-        K = nat.load().mqc_ssm_bwd_ckpt_every(code)
-        n_ckpt = (T + K - 1) // K
-        y = torch.empty(batch, T, d_inner, 4, device=Bc.device, dtype=dtype)
-        h_last = torch.empty(batch, d_inner, d_state, 4, device=Bc.device, dtype=dtype)
-        ckpt = torch.empty(batch, max(n_ckpt, 1), d_inner, d_state, 4, device=Bc.device,
-                           dtype=torch.float32)
-        nat.call("mqc_ssm_fused_fwd_train", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
-                 Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
-                 y.data_ptr(), h_last.data_ptr(), ckpt.data_ptr(), K, batch, T, d_inner,
-                 d_state, float(eps), code, nat.stream_of(Bc))
-        ctx.save_for_backward(dl, sv, Bc, Cc, la, li, Dv, h0c, ckpt)
-        ctx.meta = (eps, K, delta.dtype, s.dtype, lambda_alpha.dtype, lambda_imag.dtype,
+        y, h_last, saved = ssm_fused_dl_train_forward(delta, s, B, C, lambda_alpha,
+                                                      lambda_imag, D, h0, eps)
+        ctx.save_for_backward(*[t for t in saved if t is not None])
+        ctx.has_h0 = h0 is not None
+        ctx.meta = (eps, delta.dtype, s.dtype, lambda_alpha.dtype, lambda_imag.dtype,
                     D.dtype, None if h0 is None else h0.dtype)
         return y, h_last
 
     @staticmethod
     def backward(ctx, gy, gh_last):
-        dl, sv, Bc, Cc, la, li, Dv, h0c, ckpt = ctx.saved_tensors
-        eps, K, t_delta, t_s, t_la, t_li, t_D, t_h0 = ctx.meta
-        batch, T, d_inner, d_state, _ = Bc.shape
-        dtype = Bc.dtype
-        dev = Bc.device
-        if gy is None:
-            gy = torch.zeros(batch, T, d_inner, 4, device=dev, dtype=dtype)
-        gy = nat.aligned16(gy.to(dtype))
-        if gh_last is not None:
-            gh_last = nat.aligned16(gh_last.to(dtype))
-        d_delta = torch.empty(dl.shape, device=dev, dtype=torch.float32)
-        d_s = torch.empty(sv.shape, device=dev, dtype=torch.float32)
-        dB = torch.empty_like(Bc)
-        dC = torch.empty_like(Cc)
-        dla = torch.empty(batch, d_inner, d_state, device=dev, dtype=torch.float32)
-        dli = torch.empty(batch, d_inner, d_state, 3, device=dev, dtype=torch.float32)
-        dD = torch.empty(batch, d_inner, device=dev, dtype=torch.float32)
-        dh0 = torch.empty_like(h0c) if h0c is not None else None
-        nat.call("mqc_ssm_fused_bwd", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
-                 Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
-                 ckpt.data_ptr(), K, gy.data_ptr(), nat.ptr(gh_last), d_delta.data_ptr(),
-                 d_s.data_ptr(), dB.data_ptr(), dC.data_ptr(), dla.data_ptr(), dli.data_ptr(),
-                 dD.data_ptr(), nat.ptr(dh0), batch, T, d_inner, d_state, float(eps),
-                 nat.dtype_code(Bc), nat.stream_of(Bc))
-        return (d_delta.to(t_delta), d_s.to(t_s), dB, dC, dla.sum(0).to(t_la),
-                dli.sum(0).to(t_li), dD.sum(0).to(t_D),
-                None if dh0 is None else dh0.to(t_h0), None)
+        saved = list(ctx.saved_tensors)
+        if not ctx.has_h0:
+            saved.insert(7, None)
+        eps, t_delta, t_s, t_la, t_li, t_D, t_h0 = ctx.meta
+        d_delta, d_s, dB, dC, dla, dli, dD, dh0 = ssm_fused_dl_backward(saved, gy, gh_last, eps)
+        return (d_delta.to(t_delta), d_s.to(t_s), dB, dC, dla.to(t_la), dli.to(t_li),
+                dD.to(t_D), None if dh0 is None else dh0.to(t_h0), None)
 
 
 def ssm_forward_fused_dl(delta: torch.Tensor, s: torch.Tensor, B: torch.Tensor,

@@ -33,9 +33,11 @@ from .quat import (
     lambda_from_params,
 )
 from .block import block_forward_reference
+from .lm import lm_forward_reference
 from .complex_pair import ssm_forward_complex
 
 __all__ = [
+    "lm_forward_reference",
     "IDENTITY",
     "hamilton",
     "conjugate",

@@ -18,7 +18,18 @@ paths run:
                      where the placement of the two eps terms matters.
   * cayley.npz       cayley_discretization_reference including inputs where the
                      eps clamp of the inverse engages (|1 - z/2|^2 <= eps).
+  * lm_s1e1.npz      QuaternionMamba2 LM (vocab 37, d_model 16, 2 layers, d_state 1,
+                     expand 1; the LM configuration the reference's CPU path runs),
+                     seed 0: parameters, input ids, labels, logits and loss. Pins
+                     embedding, block stacking, final LayerNorm, head, vocab slice
+                     and the loss.
+  * init_lm.json     seed-0 constructor of QuaternionMamba2(37, d_model=16, n_layers=2,
+                     d_state=4, expand_factor=2): per-parameter shape and sha256 (the
+                     LM re-initialises nn.Linear / nn.Embedding weights in module
+                     traversal order after the blocks draw theirs).
 Fixtures are data only (npz without pickles, JSON).
+
+    python tests/golden/make_golden.py [/root/reference] [--only-lm]
 """
 from __future__ import annotations
 
@@ -31,6 +42,44 @@ import numpy as np
 import torch
 
 HERE = Path(__file__).resolve().parent
+
+
+def _param_info(module) -> dict:
+    info = {}
+    for k, v in module.state_dict().items():
+        a = v.detach().float().contiguous().numpy()
+        info[k] = {
+            "shape": list(a.shape),
+            "sha256": hashlib.sha256(a.tobytes()).hexdigest(),
+            "head": [float(t) for t in a.reshape(-1)[:4]],
+            "tail": [float(t) for t in a.reshape(-1)[-4:]],
+        }
+    return info
+
+
+def write_lm(ref_root: str) -> None:
+    sys.path.insert(0, ref_root)
+    from mambaqc.models.quaternion_mamba2 import QuaternionMamba2
+
+    torch.set_num_threads(1)
+    torch.manual_seed(0)
+    lm = QuaternionMamba2(37, d_model=16, n_layers=2, d_state=1, d_conv=4, expand_factor=1)
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, 37, (2, 9), generator=g)
+    labels = torch.randint(0, 37, (2, 9), generator=g)
+    labels[0, 3] = -100
+    with torch.no_grad():
+        out = lm(ids, labels=labels)
+    arrays = {"input_ids": ids.numpy(), "labels": labels.numpy(),
+              "logits": out["logits"].numpy(), "loss": out["loss"].numpy()}
+    for k, v in lm.state_dict().items():
+        arrays["p:" + k] = v.numpy()
+    np.savez(HERE / "lm_s1e1.npz", **arrays)
+
+    torch.manual_seed(0)
+    lm = QuaternionMamba2(37, d_model=16, n_layers=2, d_state=4, d_conv=4, expand_factor=2)
+    (HERE / "init_lm.json").write_text(json.dumps(_param_info(lm), indent=1) + "\n")
+    print("wrote lm_s1e1.npz init_lm.json")
 
 
 def main(ref_root: str = "/root/reference") -> None:
@@ -89,4 +138,9 @@ def main(ref_root: str = "/root/reference") -> None:
 
 
 if __name__ == "__main__":
-    main(*sys.argv[1:])
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    if "--only-lm" in sys.argv:
+        write_lm(*args)
+    else:
+        main(*args)
+        write_lm(*args)

@@ -157,3 +157,30 @@ def test_kernel_exports_are_functions():
         obj = getattr(K, name)
         assert not isinstance(obj, types.ModuleType), name
         assert callable(obj), name
+
+
+def test_lm_seeded_init_matches_reference():
+    """The LM re-draws every nn.Linear / nn.Embedding weight after the blocks'
+    own initialisation, in module traversal order: same parameters, bit for bit,
+    as the reference constructor under the same seed (tests/golden/init_lm.json)."""
+    info = json.loads((GOLDEN / "init_lm.json").read_text())
+    torch.manual_seed(0)
+    lm = mambaqc_amd.QuaternionMamba2(37, d_model=16, n_layers=2, d_state=4, d_conv=4,
+                                      expand_factor=2)
+    sd = lm.state_dict()
+    assert sorted(sd) == sorted(info)
+    for k, v in sd.items():
+        a = v.detach().float().contiguous().numpy()
+        assert list(a.shape) == info[k]["shape"], k
+        assert hashlib.sha256(a.tobytes()).hexdigest() == info[k]["sha256"], k
+    assert lm.vocab_size_padded == 40
+    assert lm.get_num_params() == sum(p.numel() for p in lm.parameters()) - 2 * 40 * 16
+
+
+def test_lm_presets_shapes():
+    # Constructed on the meta device: shapes only, no memory.
+    with torch.device("meta"):
+        base = mambaqc_amd.quaternion_mamba2_base(10000)
+    n = sum(p.numel() for p in base.parameters())
+    assert base.vocab_size_padded == 10000 and len(base.layers) == 12
+    assert 14.6e9 < n < 14.7e9, n  # the B/C projections dominate

@@ -322,3 +322,16 @@ def test_block_gate_slice_is_identity_at_expand_one():
     d = np.load(GOLDEN / "block_s1e1.npz")
     sd = {k[2:]: torch.from_numpy(d[k]) for k in d.files if k.startswith("p:")}
     assert sd["in_proj.weight"].shape[0] == 2 * d["x"].shape[-1]
+
+
+# ---------------------------------------------------------------- LM
+def test_lm_golden_s1e1():
+    """oracle.lm_forward_reference against the reference LM's own forward
+    (d_state 1, expand 1: the LM configuration its CPU path runs)."""
+    d = np.load(GOLDEN / "lm_s1e1.npz")
+    sd = {k[2:]: torch.from_numpy(d[k]) for k in d.files if k.startswith("p:")}
+    logits, loss = oracle.lm_forward_reference(
+        sd, torch.from_numpy(d["input_ids"]), n_layers=2, d_state=1, vocab_size=37,
+        labels=torch.from_numpy(d["labels"]))
+    torch.testing.assert_close(logits, torch.from_numpy(d["logits"]), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(loss, torch.from_numpy(d["loss"]), rtol=1e-5, atol=1e-6)
