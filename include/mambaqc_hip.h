@@ -120,6 +120,34 @@ int mqc_ssm_fused_fwd(const void* delta, const void* s, const void* B, const voi
 int mqc_qln_fwd(const void* q, const float* gamma, const float* beta, void* out, float* mean,
                 float* rstd, int64_t rows, int64_t d, float eps, int dtype, void* stream);
 
+/* Front of the block: depthwise causal conv1d (kernel `kernel` <= 8, left zero
+ * padding) fused with SiLU:
+ *   out[b,t,c] = silu(bias[c] + sum_j w[c,j] * x[b, t-(kernel-1)+j, c])
+ * x: dtype, element (b,t,c) at x[(b*seq_len + t) * x_row_stride + c] (the first
+ * half of in_proj's output is read in place); w: fp32 [channels, kernel]; bias:
+ * fp32 [channels] or NULL; out: dtype dense [batch, seq_len, channels]. (16-byte
+ * accesses when channels and x_row_stride are multiples of 16 / sizeof(dtype)
+ * and the pointers are 16-byte aligned; element accesses otherwise.)
+ * Replaces CausalConv1d.forward + F.silu, mambaqc/layers/causal_conv1d.py:68-91
+ * and mambaqc/models/quaternion_mamba2_block.py:141-144. */
+int mqc_causal_conv_silu_fwd(const void* x, int64_t x_row_stride, const float* w, const float* bias,
+                             void* out, int64_t batch, int64_t seq_len, int64_t channels,
+                             int64_t kernel, int dtype, void* stream);
+
+/* Steps per thread (R) of the conv kernels: the backward's weight partials have
+ * batch * ceil(seq_len / R) rows. */
+int mqc_conv_run_length(void);
+
+/* Backward of mqc_causal_conv_silu_fwd given gout (dtype dense [batch, seq_len,
+ * channels]): dx (dtype, rows dx_row_stride apart); dw_part fp32
+ * [batch * ceil(seq_len / R), channels, kernel] and dbias_part fp32
+ * [batch * ceil(seq_len / R), channels], R = mqc_conv_run_length(), to be
+ * summed over the first axis by the caller. */
+int mqc_causal_conv_silu_bwd(const void* x, int64_t x_row_stride, const float* w,
+                             const float* bias, const void* gout, void* dx, int64_t dx_row_stride,
+                             float* dw_part, float* dbias_part, int64_t batch, int64_t seq_len,
+                             int64_t channels, int64_t kernel, int dtype, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Training: forward with state checkpoints, and the backward passes.
  * The reference has no backward for any of its GPU kernels (its Triton launches

@@ -5,7 +5,7 @@ signature, the same parameters created in the same order (identical weights
 under the same seed, identical state_dict keys), and the same forward:
 
     xz = in_proj(x); x_in, z = chunk(xz)                    torch GEMM
-    x_act = silu(conv1d(x_in))                              torch
+    x_act = silu(conv1d(x_in))                              HIP: mqc_causal_conv_silu_fwd
     delta = softplus(dt_proj(x_act)); s = sigmoid(gate_proj(x_act)) * x_act
     B, C = B_proj(x_act), C_proj(x_act) as [B,T,D,S,4]      torch GEMMs (hipBLASLt)
     y = SSM(Cayley(delta * Lambda), B, s, C, D)             HIP: ssm_forward_fused_dl
@@ -35,7 +35,7 @@ import torch.nn.functional as F
 from . import _native as nat
 from .kernels.quaternion_norm import QuaternionLayerNorm
 from .kernels.ssm_fused import ssm_forward_fused_dl
-from .layers.causal_conv1d import CausalConv1d
+from .layers.causal_conv1d import CausalConv1d, causal_conv1d_silu
 from .layers.quaternion_linear import quaternion_to_real_projection, real_to_quaternion_projection
 
 
@@ -143,7 +143,8 @@ class QuaternionMamba2Block(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         xz = self.in_proj(x)
         x_in, z = xz.chunk(2, dim=-1)
-        x_act = F.silu(self.conv1d(x_in))
+        conv = self.conv1d.conv
+        x_act = causal_conv1d_silu(x_in, conv.weight, conv.bias)
         y = self._ssm_forward(x_act)
         y = self.norm(y)
         y_real = self.out_proj(y)
@@ -168,7 +169,9 @@ class QuaternionMamba2Block(nn.Module):
             tail, h0 = state
         xc = torch.cat([tail.to(x_in.dtype), x_in], dim=1)
         conv = self.conv1d.conv
-        x_act = F.silu(F.conv1d(xc.transpose(1, 2), conv.weight, conv.bias, groups=D).transpose(1, 2))
+        # The tail rows stand in for the zero padding: outputs from row k on
+        # are the continued convolution.
+        x_act = causal_conv1d_silu(xc, conv.weight, conv.bias)[:, k:].contiguous()
         y, h = self._ssm_forward(x_act, h0=h0, return_state=True)
         y_real = self.out_proj(self.norm(y))
         return out_gate(x, z, y_real), (xc[:, xc.shape[1] - k:], h)

@@ -11,6 +11,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .. import _native as nat
+
 
 class CausalConv1d(nn.Module):
     def __init__(self, d_model: int, kernel_size: int = 4, bias: bool = True):
@@ -36,3 +38,60 @@ class CausalConv1d(nn.Module):
 
 
 CausalConv1D = CausalConv1d
+
+
+def _rows_view(x: torch.Tensor):
+    """(x, row stride) with x's rows uniformly strided and its last axis dense;
+    otherwise a contiguous copy."""
+    B, T, C = x.shape
+    if x.stride(-1) != 1 or x.stride(0) != T * x.stride(1):
+        x = x.contiguous()
+    return x, x.stride(1)
+
+
+class _ConvSiLU(torch.autograd.Function):
+    """silu(causal depthwise conv1d(x)) with HIP forward and backward."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        B, T, C = x.shape
+        K = weight.shape[-1]
+        xv, xs = _rows_view(x.detach())
+        w = weight.detach().float().reshape(C, K).contiguous()
+        b = None if bias is None else bias.detach().float().contiguous()
+        out = torch.empty(B, T, C, device=x.device, dtype=x.dtype)
+        nat.call("mqc_causal_conv_silu_fwd", xv, xv.data_ptr(), xs, w.data_ptr(), nat.ptr(b),
+                 out.data_ptr(), B, T, C, K, nat.dtype_code(xv), nat.stream_of(xv))
+        ctx.save_for_backward(xv, w, b)
+        ctx.meta = (xs, tuple(weight.shape), weight.dtype,
+                    None if bias is None else bias.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        xv, w, b = ctx.saved_tensors
+        xs, wshape, t_w, t_b = ctx.meta
+        B, T, C = xv.shape
+        K = w.shape[1]
+        gout = nat.aligned16(gout.to(xv.dtype))
+        R = nat.load().mqc_conv_run_length()
+        rows = B * ((T + R - 1) // R)
+        dx = torch.empty(B, T, C, device=xv.device, dtype=xv.dtype)
+        dw = torch.empty(rows, C, K, device=xv.device, dtype=torch.float32)
+        db = torch.empty(rows, C, device=xv.device, dtype=torch.float32)
+        nat.call("mqc_causal_conv_silu_bwd", xv, xv.data_ptr(), xs, w.data_ptr(), nat.ptr(b),
+                 gout.data_ptr(), dx.data_ptr(), C, dw.data_ptr(), db.data_ptr(), B, T, C, K,
+                 nat.dtype_code(xv), nat.stream_of(xv))
+        return (dx, dw.sum(0).reshape(wshape).to(t_w),
+                None if t_b is None else db.sum(0).to(t_b))
+
+
+def causal_conv1d_silu(x: torch.Tensor, weight: torch.Tensor,
+                       bias: torch.Tensor | None) -> torch.Tensor:
+    """silu(CausalConv1d(x)) in one HIP pass: x [batch, seq_len, channels] (may be
+    the strided first half of in_proj's output), weight [channels, 1, k] (the
+    Conv1d's), bias [channels] or None -> dense [batch, seq_len, channels].
+    Differentiable when autograd is recording."""
+    assert x.ndim == 3 and weight.shape[0] == x.shape[-1]
+    nat.require_device("causal_conv1d_silu", x, weight)
+    return _ConvSiLU.apply(x, weight, bias)

@@ -210,3 +210,25 @@ def test_block_forward_backward_config4_fp16_autocast():
         assert a.abs().sum() > 0, n
         rel = ((a - r).norm() / r.norm()).item()
         assert rel < 5e-2, f"config 4 d{n}: fp16-autocast vs fp32 relative error {rel:.3g}"
+
+
+@pytest.mark.parametrize("shape", [(2, 37, 48, 4), (1, 3, 16, 4), (2, 20, 13, 3), (3, 33, 64, 6)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_causal_conv_silu_backward(shape, dtype):
+    from mambaqc_amd.layers.causal_conv1d import causal_conv1d_silu
+    b, T, C, K = shape
+    g = torch.Generator().manual_seed(sum(shape) + 1)
+    xz = torch.randn(b, T, 2 * C, generator=g).to(dtype)
+    w = torch.randn(C, 1, K, generator=g) * 0.5
+    bias = torch.randn(C, generator=g) * 0.1
+    gout = torch.randn(b, T, C, generator=g).to(dtype)
+    xzg, wg, bg = _leaf(xz, DEV), _leaf(w, DEV), _leaf(bias, DEV)
+    out = causal_conv1d_silu(xzg.chunk(2, dim=-1)[0], wg, bg)
+    (out.float() * gout.to(DEV).float()).sum().backward()
+    xzr, wr, br = _leaf(xz.double()), _leaf(w.double()), _leaf(bias.double())
+    xt = torch.nn.functional.pad(xzr[..., :C].transpose(1, 2), (K - 1, 0))
+    ref = torch.nn.functional.silu(torch.nn.functional.conv1d(xt, wr, br, groups=C)).transpose(1, 2)
+    (ref * gout.double()).sum().backward()
+    assert_close(xzg.grad, xzr.grad, tol(dtype), f"dx {shape} {dtype}")
+    assert_close(wg.grad, wr.grad, tol(dtype), f"dw {shape} {dtype}")
+    assert_close(bg.grad, br.grad, tol(dtype), f"dbias {shape} {dtype}")

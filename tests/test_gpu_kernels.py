@@ -346,3 +346,28 @@ def test_block_bf16_vs_oracle():
         got = blk.to(DEV)(x.to(DEV))
     assert got.dtype == torch.bfloat16
     assert_close(got, want, 2e-2, "block bf16")
+
+
+# ---------------------------------------------------------------- front of block
+def _conv_silu_ref(x, w, b):
+    """silu(CausalConv1d(x)) in float64 (layers/causal_conv1d.py:68-91 + F.silu)."""
+    C, _, K = w.shape
+    xt = torch.nn.functional.pad(x.double().transpose(1, 2), (K - 1, 0))
+    pre = torch.nn.functional.conv1d(xt, w.double(), None if b is None else b.double(), groups=C)
+    return torch.nn.functional.silu(pre).transpose(1, 2)
+
+
+@pytest.mark.parametrize("shape", [(2, 37, 48, 4), (1, 3, 16, 4), (2, 20, 13, 3), (1, 50, 24, 1),
+                                   (3, 17, 64, 6)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_causal_conv_silu(shape, dtype):
+    from mambaqc_amd.layers.causal_conv1d import causal_conv1d_silu
+    b, T, C, K = shape
+    g = torch.Generator().manual_seed(sum(shape))
+    xz = torch.randn(b, T, 2 * C, generator=g).to(dtype)
+    w = torch.randn(C, 1, K, generator=g) * 0.5
+    bias = torch.randn(C, generator=g) * 0.1
+    x_in = xz.to(DEV).chunk(2, dim=-1)[0]                 # strided view, row stride 2C
+    got = causal_conv1d_silu(x_in, w.to(DEV), bias.to(DEV))
+    assert got.is_contiguous() and got.dtype == dtype
+    assert_close(got, _conv_silu_ref(xz[..., :C], w, bias), tol(dtype), f"conv_silu {shape} {dtype}")
