@@ -44,16 +44,17 @@ __device__ inline void st(T* __restrict__ p, const float (&r)[V]) {
   else store_vec<T, V>(p, r);
 }
 
-// Load V channels of row t (zeros outside [0, T)).
+// Load V channels of row t (zeros outside [0, T)). The row is clamped onto a
+// valid one and the value masked, so the load carries no predicate and the
+// loads of a run issue back to back.
 template <typename T, int V>
 __device__ inline void conv_row(const T* __restrict__ x, int64_t xs, int64_t b, int64_t T_len,
                                 int64_t t, int64_t c, float (&r)[V]) {
-  if (t < 0 || t >= T_len) {
+  const bool in = t >= 0 && t < T_len;
+  const int64_t tc = t < 0 ? 0 : (t < T_len ? t : T_len - 1);
+  ld<T, V>(x + (b * T_len + tc) * xs + c, r);
 #pragma unroll
-    for (int v = 0; v < V; ++v) r[v] = 0.f;
-  } else {
-    ld<T, V>(x + (b * T_len + t) * xs + c, r);
-  }
+  for (int v = 0; v < V; ++v) r[v] = in ? r[v] : 0.f;
 }
 
 template <typename T, int K, int TR, int V>
@@ -82,7 +83,6 @@ __global__ __launch_bounds__(kConvThreads) void conv_silu_fwd_kernel(
 #pragma unroll
   for (int i = 0; i < TR; ++i) {
     const int64_t t = t0 + i;
-    if (t >= T_len) continue;
     conv_row<T, V>(x, xs, b, T_len, t, c, win[K - 1]);
     float o[V];
 #pragma unroll
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(kConvThreads) void conv_silu_fwd_kernel(
       for (int j = 0; j < K; ++j) p = fmaf(wk[j][v], win[j][v], p);
       o[v] = p * sigmoid_f(p);
     }
-    st<T, V>(out + (b * T_len + t) * C + c, o);
+    if (t < T_len) st<T, V>(out + (b * T_len + t) * C + c, o);
 #pragma unroll
     for (int j = 0; j < K - 1; ++j)
 #pragma unroll
@@ -139,33 +139,35 @@ __global__ __launch_bounds__(kConvThreads) void conv_silu_bwd_kernel(
 #pragma unroll
   for (int j = 1; j < K; ++j) {
     const int64_t tt = t_end - 1 + j;
+    const bool in = tt < T_len;
+    const int64_t tc = in ? tt : T_len - 1;
+    float xw[K][V];
 #pragma unroll
-    for (int v = 0; v < V; ++v) gpw[j][v] = 0.f;
-    if (tt < T_len) {
-      float xw[K][V];
+    for (int q = 0; q < K; ++q) conv_row<T, V>(x, xs, b, T_len, tc - (K - 1) + q, c, xw[q]);
+    float g[V];
+    ld<T, V>(gout + (b * T_len + tc) * C + c, g);
 #pragma unroll
-      for (int q = 0; q < K; ++q) conv_row<T, V>(x, xs, b, T_len, tt - (K - 1) + q, c, xw[q]);
-      float g[V];
-      ld<T, V>(gout + (b * T_len + tt) * C + c, g);
+    for (int v = 0; v < V; ++v) {
+      float p = bs[v];
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        float p = bs[v];
-#pragma unroll
-        for (int q = 0; q < K; ++q) p = fmaf(wk[q][v], xw[q][v], p);
-        const float sg = sigmoid_f(p);
-        gpw[j][v] = g[v] * sg * (1.f + p * (1.f - sg));
-      }
+      for (int q = 0; q < K; ++q) p = fmaf(wk[q][v], xw[q][v], p);
+      const float sg = sigmoid_f(p);
+      gpw[j][v] = in ? g[v] * sg * (1.f + p * (1.f - sg)) : 0.f;
     }
   }
 #pragma unroll
   for (int i = TR - 1; i >= 0; --i) {
     const int64_t t = t0 + i;
-    if (t >= T_len) continue;
+    // Steps past T (the last run only) are computed on a clamped row and
+    // discarded: they contribute nothing and do not shift the window.
+    const bool live = t < T_len;
+    const int64_t tc = live ? t : T_len - 1;
     float xw[K][V];
 #pragma unroll
-    for (int q = 0; q < K; ++q) conv_row<T, V>(x, xs, b, T_len, t - (K - 1) + q, c, xw[q]);
+    for (int q = 0; q < K; ++q) conv_row<T, V>(x, xs, b, T_len, tc - (K - 1) + q, c, xw[q]);
     float g[V];
-    ld<T, V>(gout + (b * T_len + t) * C + c, g);
+    ld<T, V>(gout + (b * T_len + tc) * C + c, g);
+    if (!live) continue;
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       float p = bs[v];

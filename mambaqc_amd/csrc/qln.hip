@@ -54,34 +54,38 @@ __global__ __launch_bounds__(256) void qln_kernel(const T* __restrict__ q,
   const int64_t row = (int64_t)blockIdx.x * RPB + sub;
   const bool rvalid = row < rows;
   constexpr int TPR = 64 * WPR;
-  const T* qr = q + (rvalid ? row : 0) * d * 4;
+  // Rows and elements past the end are clamped onto valid addresses (and their
+  // values masked), so the NPL loads carry no predicate and issue back to back.
+  const T* qr = q + (rvalid ? row : rows - 1) * d * 4;
 
   float v[NPL][4];
   float n[NPL];
 #pragma unroll
   for (int m = 0; m < NPL; ++m) {
     const int64_t i = t + (int64_t)m * TPR;
-    if (rvalid && i < d) {
-      load_vec<T, 4>(qr + i * 4, v[m]);
-    } else {
-      v[m][0] = v[m][1] = v[m][2] = v[m][3] = 0.f;
-    }
+    load_vec<T, 4>(qr + (i < d ? i : d - 1) * 4, v[m]);
+  }
+#pragma unroll
+  for (int m = 0; m < NPL; ++m) {
+    const bool in = t + (int64_t)m * TPR < d;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[m][c] = in ? v[m][c] : 0.f;
   }
   float s1 = 0.f;
 #pragma unroll
   for (int m = 0; m < NPL; ++m) {
-    const int64_t i = t + (int64_t)m * TPR;
+    const bool in = t + (int64_t)m * TPR < d;
     n[m] = sqrtf(v[m][0] * v[m][0] + v[m][1] * v[m][1] + v[m][2] * v[m][2] + v[m][3] * v[m][3] + eps);
-    if (i < d) s1 += n[m];
+    s1 += in ? n[m] : 0.f;
   }
   const float inv_d = 1.f / (float)d;
   const float mu = row_sum<WPR>(s1, red[sub]) * inv_d;
   float s2 = 0.f;
 #pragma unroll
   for (int m = 0; m < NPL; ++m) {
-    const int64_t i = t + (int64_t)m * TPR;
+    const bool in = t + (int64_t)m * TPR < d;
     const float c = n[m] - mu;
-    if (i < d) s2 = fmaf(c, c, s2);
+    s2 = in ? fmaf(c, c, s2) : s2;
   }
   const float var = row_sum<WPR>(s2, red[sub]) * inv_d;
   const float rstd = 1.f / sqrtf(var + eps);
@@ -95,13 +99,12 @@ __global__ __launch_bounds__(256) void qln_kernel(const T* __restrict__ q,
 #pragma unroll
     for (int m = 0; m < NPL; ++m) {
       const int64_t i = t + (int64_t)m * TPR;
-      if (i < d) {
-        const float f = gamma[i] * ((n[m] - mu) * rstd) / (n[m] + eps);
-        const float4 bt = reinterpret_cast<const float4*>(beta)[i];
-        float o[4] = {fmaf(f, v[m][0], bt.x), fmaf(f, v[m][1], bt.y), fmaf(f, v[m][2], bt.z),
-                      fmaf(f, v[m][3], bt.w)};
-        store_vec<T, 4>(orow + i * 4, o);
-      }
+      const int64_t ic = i < d ? i : d - 1;
+      const float f = gamma[ic] * ((n[m] - mu) * rstd) / (n[m] + eps);
+      const float4 bt = reinterpret_cast<const float4*>(beta)[ic];
+      float o[4] = {fmaf(f, v[m][0], bt.x), fmaf(f, v[m][1], bt.y), fmaf(f, v[m][2], bt.z),
+                    fmaf(f, v[m][3], bt.w)};
+      if (i < d) store_vec<T, 4>(orow + i * 4, o);
     }
   }
 }
@@ -169,7 +172,8 @@ __global__ __launch_bounds__(256) void qln_bwd_kernel(const T* __restrict__ q,
   const int64_t row = (int64_t)blockIdx.x * RPB + sub;
   const bool rvalid = row < rows;
   constexpr int TPR = 64 * WPR;
-  const int64_t r = rvalid ? row : 0;
+  // Clamped rows and elements (values masked) keep the loads unpredicated.
+  const int64_t r = rvalid ? row : rows - 1;
   const T* qr = q + r * d * 4;
   const T* gr = dout + r * d * 4;
   const float mu = mean[r];
@@ -181,12 +185,17 @@ __global__ __launch_bounds__(256) void qln_bwd_kernel(const T* __restrict__ q,
 #pragma unroll
   for (int m = 0; m < NPL; ++m) {
     const int64_t i = t + (int64_t)m * TPR;
-    if (rvalid && i < d) {
-      load_vec<T, 4>(qr + i * 4, v[m]);
-      load_vec<T, 4>(gr + i * 4, g[m]);
-    } else {
+    const int64_t ic = i < d ? i : d - 1;
+    load_vec<T, 4>(qr + ic * 4, v[m]);
+    load_vec<T, 4>(gr + ic * 4, g[m]);
+  }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) { v[m][c] = 0.f; g[m][c] = 0.f; }
+  for (int m = 0; m < NPL; ++m) {
+    const bool in = t + (int64_t)m * TPR < d;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      v[m][c] = in ? v[m][c] : 0.f;
+      g[m][c] = in ? g[m][c] : 0.f;
     }
   }
 #pragma unroll
@@ -199,7 +208,8 @@ __global__ __launch_bounds__(256) void qln_bwd_kernel(const T* __restrict__ q,
     nh[m] = (n - mu) * rstd;
     e[m] = (g[m][0] * v[m][0] + g[m][1] * v[m][1] + g[m][2] * v[m][2] + g[m][3] * v[m][3]) *
            inv_ne[m];
-    const float dnh = in ? gamma[i] * e[m] : 0.f;
+    const float gmv = gamma[in ? i : d - 1];
+    const float dnh = in ? gmv * e[m] : 0.f;
     s1 += dnh;
     s2 = fmaf(dnh, nh[m], s2);
   }
@@ -212,8 +222,8 @@ __global__ __launch_bounds__(256) void qln_bwd_kernel(const T* __restrict__ q,
 #pragma unroll
   for (int m = 0; m < NPL; ++m) {
     const int64_t i = t + (int64_t)m * TPR;
+    const float gm = gamma[i < d ? i : d - 1];
     if (i < d) {
-      const float gm = gamma[i];
       const float n = sqrtf(v[m][0] * v[m][0] + v[m][1] * v[m][1] + v[m][2] * v[m][2] +
                             v[m][3] * v[m][3] + eps);
       const float a = gm * nh[m] * inv_ne[m];                 // coefficient of dout
