@@ -31,7 +31,9 @@ __global__ __launch_bounds__(W * 64) void cumprod_scan_kernel(const T* __restric
   const int64_t b = blockIdx.y;
   const bool valid = l < L;
   const int64_t row = L * 4;  // elements per (b, t)
-  const T* qb = q + b * T_len * row + l * 4;
+  // Lanes past L and steps past T load from clamped (valid) addresses and use
+  // the identity instead, so the loads carry no predicate and issue together.
+  const T* qb = q + b * T_len * row + (valid ? l : L - 1) * 4;
   T* ob = out + b * T_len * row + l * 4;
 
   if (w == 0) carry[lane] = make_float4(1.f, 0.f, 0.f, 0.f);
@@ -44,13 +46,12 @@ __global__ __launch_bounds__(W * 64) void cumprod_scan_kernel(const T* __restric
     quat v[TW];
 #pragma unroll
     for (int j = 0; j < TW; ++j) {
-      if (valid && j < n) {
-        float e[4];
-        load_vec<T, 4>(qb + (t0 + j) * row, e);
-        v[j] = quat_from(e);
-      } else {
-        v[j] = quat{1.f, 0.f, 0.f, 0.f};
-      }
+      int64_t tj = t0 + j;
+      tj = tj < T_len ? tj : T_len - 1;
+      float e[4];
+      load_vec<T, 4>(qb + tj * row, e);
+      const bool use = valid && j < n;
+      v[j] = use ? quat_from(e) : quat{1.f, 0.f, 0.f, 0.f};
     }
     // Local inclusive prefixes: v[j] <- q_j (x) v[j-1].
 #pragma unroll

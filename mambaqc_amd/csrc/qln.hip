@@ -134,10 +134,10 @@ int launch_qln(const void* q, const float* gamma, const float* beta, void* out, 
   MQC_QLN(1, 1)
   MQC_QLN(2, 1)
   MQC_QLN(4, 1)
-  MQC_QLN(8, 1)
-  MQC_QLN(16, 1)
-  MQC_QLN(24, 1)
-  MQC_QLN(32, 1)
+  MQC_QLN(2, 4)
+  MQC_QLN(4, 4)
+  MQC_QLN(6, 4)
+  MQC_QLN(8, 4)
   MQC_QLN(16, 4)
   MQC_QLN(32, 4)
 #undef MQC_QLN
