@@ -142,6 +142,67 @@ def cpu_baseline(blk, x, t_sample=128):
     }
 
 
+def cpu_components():
+    """The rest of the CPU baseline plan: the oracle (fp32 torch on the host's
+    cores) on bounded samples of configs 1-3, median of 3 after one warm-up.
+    GB/s figures use the same algorithmic bytes as the GPU kernels."""
+    import torch
+    import torch.nn.functional as F
+    import mambaqc_amd
+    import oracle
+
+    def med(fn):
+        fn()
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[1]
+
+    out = {}
+    g = torch.Generator().manual_seed(0)
+    # Config 1: the whole block, B1 T64 d64 s16.
+    torch.manual_seed(0)
+    blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=16, d_conv=4, expand_factor=2)
+    sd = blk.state_dict()
+    x1 = torch.randn(1, 64, 64, generator=g)
+    sec = med(lambda: oracle.block_forward_reference(sd, x1, d_state=16))
+    out["c1_block_fwd_tokens_s"] = round(64 / sec, 1)
+    # Config 2 on a slice of 96 of the 768 d's (all of B, T, S): Cayley, then the scan.
+    shape = (2, 256, 96, 64)
+    n = lambda: torch.randn(*shape, generator=g)
+    z = torch.empty(*shape, 4)
+    z[..., 0] = -torch.exp(n()) * F.softplus(n())
+    for c in range(1, 4):
+        z[..., c] = n() * F.softplus(n())
+    nbytes = 2 * z.numel() * 4
+    sec = med(lambda: oracle.cayley_reference(z))
+    out["c2_cayley_GBs"] = round(nbytes / sec / 1e9, 3)
+    q = oracle.cayley_reference(z)
+    sec = med(lambda: oracle.cumprod_reference(q))
+    out["c2_cumprod_GBs"] = round(nbytes / sec / 1e9, 3)
+    del z, q
+    # Config 3 SSM + QLN on B1, the first 32 steps, 64 of the 1536 d's (S = 64).
+    Bt, Tt, Dt, St = 1, 32, 64, 64
+    delta = F.softplus(torch.randn(Bt, Tt, Dt, generator=g) - 2)
+    sv = torch.randn(Bt, Tt, Dt, generator=g)
+    Bq = torch.randn(Bt, Tt, Dt, St, 4, generator=g) * 0.02
+    Cq = torch.randn(Bt, Tt, Dt, St, 4, generator=g) * 0.02
+    la = torch.randn(Dt, St, generator=g) * 0.5 + 1
+    li = torch.randn(Dt, St, 3, generator=g) * 0.1
+    Dv, gm, bt = torch.ones(Dt), torch.ones(Dt), torch.zeros(Dt, 4)
+    sec = med(lambda: oracle.qln_reference(
+        oracle.ssm_forward_dl_reference(delta, sv, Bq, Cq, la, li, Dv), gm, bt))
+    lanes = Bt * Tt * Dt
+    out["c3_ssm_qln_lane_steps_per_s"] = round(lanes * St / sec, 1)
+    out["c3_ssm_qln_equiv_tokens_s"] = round(lanes * St / sec / (DI * DS), 3)
+    out["samples"] = ("c1: whole block B1 T64 d64 s16; c2: [2,256,96,64,4] fp32 (96 of 768 d's) "
+                      "Cayley then cumprod; c3: SSM+QLN on B1 T32, 64 of 1536 d's, S64, "
+                      "equiv_tokens_s = (b,t,d,k) lane-steps per s / (1536 * 64)")
+    return out
+
+
 def read_traffic():
     """HBM bytes per launch of the SSM kernel from the committed rocprofv3 PMC
     summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor)."""
@@ -224,6 +285,8 @@ def run_full(args):
     base = None if args.no_cpu else cpu_baseline(blk, x)
     if base:
         log(f"cpu baseline: {base['value']} tokens/s on {base['cores']} threads")
+        base["components"] = cpu_components()
+        log(f"cpu components: {base['components']}")
 
     result = {
         "metric": METRIC,
