@@ -22,8 +22,7 @@
 // states from the previous checkpoint into registers (same arithmetic as the
 // forward), then runs the adjoint steps above in reverse. One lane owns one
 // (b, d, k); a group of G lanes owns a (b, d) and sums d delta and ds over k
-// with the same VALU reduction as the forward. 768-thread blocks run in
-// lockstep (a barrier per chunk), like the forward.
+// with the same VALU reduction as the forward.
 #pragma once
 
 #include "ssm_scan.hpp"
@@ -111,7 +110,13 @@ __device__ inline void group_reduce2(float& u, float& w, int lane) {
   }
 }
 
-template <typename T, int G, int K, int NT, bool FULL>
+// SYNC: a block barrier after every chunk keeps the block's waves on the same
+// chunk. Unlike the forward, the backward gains nothing from it: it is VALU
+// bound (about 220 VALU instructions per step and lane, 4.6 ms of issue at
+// config 3 against 5 ms of HBM traffic), so the launcher runs free 256-thread
+// blocks, measured 4 % faster than lockstep 768-thread ones. Double-buffering
+// the chunk operands was measured too and gave nothing at K = 8.
+template <typename T, int G, int K, int NT, bool FULL, bool SYNC>
 __global__ __launch_bounds__(NT) void ssm_bwd_kernel(SsmBwdArgs a) {
   static_assert((G & (G - 1)) == 0 && G <= 64 && NT % 64 == 0 && NT % G == 0, "bad group");
   constexpr int GPB = NT / G;
@@ -148,27 +153,36 @@ __global__ __launch_bounds__(NT) void ssm_bwd_kernel(SsmBwdArgs a) {
     carry = quat_from(e);
   }
 
-  for (int64_t c = nC - 1; c >= 0; --c) {
-    const int64_t t0 = c * K;
-    const int len = (int)(Tn - t0 < K ? Tn - t0 : K);
-    // Operands of the chunk (the tail chunk re-reads its last step).
+  // Operands of one chunk: the K steps' delta, s, B, C, gy (raw bits) and the
+  // checkpointed state before the chunk.
+  struct Ops {
     Raw<T, 1> rd[K], rs[K];
     Raw<T, 4> rB[K], rC[K], rg[K];
+    float4 h_in;
+  };
+  auto load_chunk = [&](Ops& o, int64_t c) {
+    const int64_t t0 = c * K;
+    const int len = (int)(Tn - t0 < K ? Tn - t0 : K);
 #pragma unroll
     for (int i = 0; i < K; ++i) {
+      // The tail chunk re-reads its last step.
       const int64_t rt = b * Tn + t0 + (i < len ? i : len - 1);
-      raw_load<T, 1>((const char*)((const T*)a.delta + rt * rowTok) + offTok, rd[i]);
-      raw_load<T, 1>((const char*)((const T*)a.s + rt * rowTok) + offTok, rs[i]);
-      raw_load<T, 4>((const char*)((const T*)a.Bm + rt * rowBC) + offBC, rB[i]);
-      raw_load<T, 4>((const char*)((const T*)a.Cm + rt * rowBC) + offBC, rC[i]);
-      raw_load<T, 4>((const char*)((const T*)a.gy + rt * rowY) + offY, rg[i]);
+      raw_load<T, 1>((const char*)((const T*)a.delta + rt * rowTok) + offTok, o.rd[i]);
+      raw_load<T, 1>((const char*)((const T*)a.s + rt * rowTok) + offTok, o.rs[i]);
+      raw_load<T, 4>((const char*)((const T*)a.Bm + rt * rowBC) + offBC, o.rB[i]);
+      raw_load<T, 4>((const char*)((const T*)a.Cm + rt * rowBC) + offBC, o.rC[i]);
+      raw_load<T, 4>((const char*)((const T*)a.gy + rt * rowY) + offY, o.rg[i]);
     }
-    // State before the chunk: the previous chunk's checkpoint, or h0.
+    // The checkpoint of the previous chunk (chunk 0 starts from h0, read in process).
+    const int64_t cp = c > 0 ? c - 1 : 0;
+    o.h_in = *reinterpret_cast<const float4*>(a.h_ckpt + (((b * nC + cp) * a.Dm + d) * a.S + k) * 4);
+  };
+  auto process_chunk = [&](Ops& o, int64_t c) {
+    const int64_t t0 = c * K;
+    const int len = (int)(Tn - t0 < K ? Tn - t0 : K);
     quat hs[K + 1];
     if (c > 0) {
-      const float4 v = *reinterpret_cast<const float4*>(
-          a.h_ckpt + (((b * nC + (c - 1)) * a.Dm + d) * a.S + k) * 4);
-      hs[0] = quat{v.x, v.y, v.z, v.w};
+      hs[0] = quat{o.h_in.x, o.h_in.y, o.h_in.z, o.h_in.w};
     } else if (a.h0) {
       float e[4];
       load_vec<T, 4>((const T*)a.h0 + sidx, e);
@@ -180,9 +194,9 @@ __global__ __launch_bounds__(NT) void ssm_bwd_kernel(SsmBwdArgs a) {
 #pragma unroll
     for (int i = 0; i < K; ++i) {
       if (i < len) {
-        const float dl = raw_get(rd[i], 0);
+        const float dl = raw_get(o.rd[i], 0);
         const quat q = cayley_step(dl, dl * dl, L, a.eps);
-        hs[i + 1] = state_step(q, hs[i], raw_get(rs[i], 0), raw_quat(rB[i], 0));
+        hs[i + 1] = state_step(q, hs[i], raw_get(o.rs[i], 0), raw_quat(o.rB[i], 0));
       }
     }
     // Adjoint steps, last to first.
@@ -190,13 +204,13 @@ __global__ __launch_bounds__(NT) void ssm_bwd_kernel(SsmBwdArgs a) {
     for (int i = K - 1; i >= 0; --i) {
       if (i < len) {
         const int64_t rt = b * Tn + t0 + i;
-        const float dl = raw_get(rd[i], 0);
+        const float dl = raw_get(o.rd[i], 0);
         const float dl2 = dl * dl;
-        const float sv = raw_get(rs[i], 0);
+        const float sv = raw_get(o.rs[i], 0);
         const quat q = cayley_step(dl, dl2, L, a.eps);
-        const quat gy = raw_quat(rg[i], 0);
-        const quat Ck = raw_quat(rC[i], 0);
-        const quat Bk = raw_quat(rB[i], 0);
+        const quat gy = raw_quat(o.rg[i], 0);
+        const quat Ck = raw_quat(o.rC[i], 0);
+        const quat Bk = raw_quat(o.rB[i], 0);
         quat g = carry;
         qmul_acc(g, qconj(Ck), gy);
         quat dq{0.f, 0.f, 0.f, 0.f};
@@ -226,7 +240,13 @@ __global__ __launch_bounds__(NT) void ssm_bwd_kernel(SsmBwdArgs a) {
         }
       }
     }
-    __syncthreads();
+    if constexpr (SYNC) __syncthreads();
+  };
+
+  Ops buf;
+  for (int64_t c = nC - 1; c >= 0; --c) {
+    load_chunk(buf, c);
+    process_chunk(buf, c);
   }
 
   if (own) {
@@ -254,15 +274,15 @@ constexpr int ssm_bwd_chunk() { return sizeof(T) == 4 ? 4 : 8; }
 template <typename T, int G>
 int launch_ssm_bwd_g(const SsmBwdArgs& a, hipStream_t s) {
   constexpr int K = ssm_bwd_chunk<T>();
-  constexpr int NT = G >= 8 ? 768 : 256;
+  constexpr int NT = 256;
   constexpr int GPB = NT / G;
   const int64_t gx = (a.Dm + GPB - 1) / GPB;
   if (gx > 0x7fffffffLL || a.batch > 65535) return MQC_E_LIMIT;
   const dim3 grid((unsigned)gx, (unsigned)a.batch);
   if (a.S == G)
-    ssm_bwd_kernel<T, G, K, NT, true><<<grid, dim3(NT), 0, s>>>(a);
+    ssm_bwd_kernel<T, G, K, NT, true, false><<<grid, dim3(NT), 0, s>>>(a);
   else
-    ssm_bwd_kernel<T, G, K, NT, false><<<grid, dim3(NT), 0, s>>>(a);
+    ssm_bwd_kernel<T, G, K, NT, false, false><<<grid, dim3(NT), 0, s>>>(a);
   return launch_status();
 }
 
