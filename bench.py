@@ -417,11 +417,21 @@ def lm_timing(args):
     n_params = sum(p.numel() for p in lm.parameters())
     log(f"config 5 LM forward ({n_params / 1e9:.2f} B params, bf16): {ms:.1f} ms, "
         f"{B * T / ms * 1e3:.0f} tokens/s")
-    del lm
+    # Recurrent decoding after the 2048-token prompt: one step per new token
+    # (the reference re-runs the whole sequence instead).
+    with torch.inference_mode():
+        _, states = lm.forward_with_state(ids)
+        tok = ids[:, -1:]
+        lm.forward_with_state(tok, states)
+        dec_ms = event_time_ms(lambda: lm.forward_with_state(tok, states), 20)
+    log(f"config 5 recurrent decode: {dec_ms:.2f} ms per step of {B} tokens")
+    del lm, states
     torch.cuda.empty_cache()
     return {"workload": "QuaternionMamba2 base (12 layers) forward, bf16, B4 T2048, vocab 10000",
             "params": n_params, "ms_per_step": round(ms, 2),
-            "tokens_per_s": round(B * T / ms * 1e3, 1)}
+            "tokens_per_s": round(B * T / ms * 1e3, 1),
+            "decode_ms_per_token_step": round(dec_ms, 3),
+            "decode_tokens_per_s": round(B / dec_ms * 1e3, 1)}
 
 
 def run_kernel_loop(args):
@@ -470,6 +480,19 @@ def run_kernel_loop(args):
             bt = torch.zeros(DI, 4, device="cuda")
             fn = lambda: K.quaternion_layer_norm_fused(y, gm, bt)
             nbytes = qln_bytes(B * T, DI)
+        elif args.mode == "decode":
+            # Recurrent decoding with the base preset: prompt of 64 tokens, then
+            # one step per token through every block (bf16, batch 4).
+            import mambaqc_amd
+            torch.manual_seed(0)
+            with torch.device("cuda"):
+                lm = mambaqc_amd.quaternion_mamba2_base(10000)
+            lm = lm.to(torch.bfloat16).eval()
+            ids = torch.randint(0, 10000, (B, 64), generator=g, device="cuda")
+            _, states = lm.forward_with_state(ids)
+            tok = ids[:, -1:]
+            fn = lambda: lm.forward_with_state(tok, states)
+            nbytes = sum(p.numel() * p.element_size() for p in lm.parameters())
         elif args.mode == "copy":
             src = torch.empty(1 << 28, device="cuda")  # 1 GiB
             dst = torch.empty_like(src)
