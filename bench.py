@@ -215,6 +215,21 @@ def read_traffic():
     return None
 
 
+def box_copy_gbs(reps=10):
+    """Read+write bandwidth of a 1 GiB device-to-device copy on this box. HBM
+    throughput differs from box to box by up to ~15 %; this puts the SSM's
+    figure beside what a plain copy gets on the same device."""
+    import torch
+
+    src = torch.empty(1 << 28, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    ms = event_time_ms(lambda: dst.copy_(src), reps)
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * (1 << 30) / (ms * 1e-3) / 1e9
+
+
 def run_full(args):
     import torch
     from mambaqc_amd import kernels as K
@@ -262,6 +277,9 @@ def run_full(args):
     qln_gbs = qln_bytes(B * T, DI) / (stages["qln"] * 1e-3) / 1e9
     del delta, s, Bq, Cq
     torch.cuda.empty_cache()
+    copy_gbs = box_copy_gbs()
+    log(f"box calibration: 1 GiB device copy {copy_gbs:.0f} GB/s; fused SSM at "
+        f"{achieved / copy_gbs:.1%} of it")
 
     # Config 2 standalone: Cayley then cumprod, fp32 [2,256,768,64,4].
     shape = (2, 256, 768, 64)
@@ -316,6 +334,8 @@ def run_full(args):
             "traffic": read_traffic(),
             "algorithmic_bytes": nbytes,
             "mean_launch_ms": round(ssm_ms, 4),
+            "box_copy_GBs": round(copy_gbs, 1),
+            "frac_of_box_copy": round(achieved / copy_gbs, 4),
         },
         "stages_ms": {k: round(v, 4) for k, v in stages.items()},
         "components": {

@@ -215,6 +215,24 @@ int mqc_out_gate_bwd(const void* dout, const void* z, int64_t z_row_stride, cons
 int mqc_out_gate_fwd(const void* x, const void* z, int64_t z_row_stride, const void* y_real,
                      void* out, int64_t rows, int64_t cols, int dtype, void* stream);
 
+/* Front of the block's SSM over n elements of same-shaped contiguous tensors:
+ *   delta = softplus(dt_raw)   (identity above 20, torch's threshold)
+ *   s     = sigmoid(g_raw) * x
+ * dt_raw, g_raw, x, delta, s: dtype. dt_raw is dt_proj's output (bias added),
+ * g_raw gate_proj's. Replaces mambaqc/models/quaternion_mamba2_block.py:183
+ * (Delta = F.softplus(self.dt_proj(x))) and :197-198 (gate * x). */
+int mqc_ssm_front_fwd(const void* dt_raw, const void* g_raw, const void* x, void* delta, void* s,
+                      int64_t n, int dtype, void* stream);
+
+/* Backward of mqc_ssm_front_fwd from fp32 d_delta, d_s [n]:
+ *   d_dt_raw = d_delta * sigmoid(dt_raw) (d_delta above 20),
+ *   d_g_raw = d_s * x * sigmoid'(g_raw),  d_x = d_s * sigmoid(g_raw)
+ * (d_x is the part of x's gradient that flows through s). Outputs: dtype [n].
+ * The reference runs these through torch autograd (same lines as the forward). */
+int mqc_ssm_front_bwd(const void* dt_raw, const void* g_raw, const void* x, const float* d_delta,
+                      const float* d_s, void* d_dt_raw, void* d_g_raw, void* d_x, int64_t n,
+                      int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

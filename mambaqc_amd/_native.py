@@ -48,13 +48,15 @@ SIGNATURES = {
                           _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _int, _vp],
     "mqc_qln_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _int, _vp],
     "mqc_out_gate_bwd": [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
+    "mqc_ssm_front_fwd": [_vp, _vp, _vp, _vp, _vp, _i64, _int, _vp],
+    "mqc_ssm_front_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _int, _vp],
     "mqc_causal_conv_silu_fwd": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp],
     "mqc_conv_run_length": [],
     "mqc_causal_conv_silu_bwd": [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64,
                                  _i64, _i64, _int, _vp],
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib = None

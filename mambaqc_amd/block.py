@@ -6,18 +6,20 @@ under the same seed, identical state_dict keys), and the same forward:
 
     xz = in_proj(x); x_in, z = chunk(xz)                    torch GEMM
     x_act = silu(conv1d(x_in))                              HIP: mqc_causal_conv_silu_fwd
-    delta = softplus(dt_proj(x_act)); s = sigmoid(gate_proj(x_act)) * x_act
+    dt_raw, g_raw = dt_proj(x_act), gate_proj(x_act)        torch GEMMs
+    delta = softplus(dt_raw); s = sigmoid(g_raw) * x_act    HIP: mqc_ssm_front_fwd
     B, C = B_proj(x_act), C_proj(x_act) as [B,T,D,S,4]      torch GEMMs (hipBLASLt)
-    y = SSM(Cayley(delta * Lambda), B, s, C, D)             HIP: ssm_forward_fused_dl
+    y = SSM(Cayley(delta * Lambda), B, s, C, D)             HIP: mqc_ssm_fused_fwd
     y = QuaternionLayerNorm(y)                              HIP: mqc_qln_fwd
     y_real = out_proj(y)                                    torch GEMM
     out = x + sigmoid(z[..., :d_model]) * y_real            HIP: mqc_out_gate_fwd
 
 z, q and the quaternion S are never materialised: the SSM kernel discretises
 in registers and takes the real selected signal s. When autograd is recording,
-the SSM, QLN and gate run as torch.autograd.Functions with HIP backward
-kernels (the reference's GPU path has no backward: its Triton launches sit
-outside autograd); the GEMMs, conv and activations use torch's autograd.
+the front (softplus, sigmoid gate) + SSM, the conv + SiLU, QLN and gate run
+as torch.autograd.Functions with HIP backward kernels (the reference's GPU
+path has no backward: its Triton launches sit outside autograd); the GEMMs
+use torch's autograd.
 
 The gate uses z[..., :d_model]. The reference multiplies sigmoid(z), which has
 d_inner = expand_factor * d_model features, by y_real, which has d_model
@@ -30,11 +32,10 @@ from __future__ import annotations
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import _native as nat
 from .kernels.quaternion_norm import QuaternionLayerNorm
-from .kernels.ssm_fused import ssm_forward_fused_dl
+from .kernels.ssm_fused import ssm_forward_front_dl
 from .layers.causal_conv1d import CausalConv1d, causal_conv1d_silu
 from .layers.quaternion_linear import quaternion_to_real_projection, real_to_quaternion_projection
 
@@ -180,12 +181,13 @@ class QuaternionMamba2Block(nn.Module):
                      return_state: bool = False):
         """x: [batch, seq_len, d_inner] (real) -> y: [batch, seq_len, d_inner, 4]."""
         b, t, D = x.shape
-        delta = F.softplus(self.dt_proj(x))
+        dt_raw = self.dt_proj(x)
         Bq = self.B_proj(x).view(b, t, D, self.d_state, 4)
         Cq = self.C_proj(x).view(b, t, D, self.d_state, 4)
-        s = torch.sigmoid(self.gate_proj(x)) * x
-        return ssm_forward_fused_dl(delta, s, Bq, Cq, self.Lambda_alpha, self.Lambda_imag,
-                                    self.D, eps=1e-6, h0=h0, return_state=return_state)
+        g_raw = self.gate_proj(x)
+        return ssm_forward_front_dl(dt_raw, g_raw, x, Bq, Cq, self.Lambda_alpha,
+                                    self.Lambda_imag, self.D, eps=1e-6, h0=h0,
+                                    return_state=return_state)
 
     def extra_repr(self) -> str:
         return (f"d_model={self.d_model}, d_state={self.d_state}, d_inner={self.d_inner}, "

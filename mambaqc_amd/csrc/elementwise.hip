@@ -275,6 +275,132 @@ int launch_out_gate_bwd(const void* dout, const void* z, int64_t zs, const void*
   return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// Front of the SSM, over n elements of same-shaped contiguous tensors:
+//   delta = softplus(dt_raw)      (torch's threshold 20: identity above it)
+//   s     = sigmoid(g_raw) * x
+// and its backward from fp32 d_delta, d_s:
+//   d_dt_raw = d_delta * sigmoid(dt_raw)   (1 above the threshold)
+//   d_g_raw  = d_s * x * sig(g) * (1 - sig(g)),   d_x = d_s * sig(g)
+// ---------------------------------------------------------------------------
+__device__ inline float front_softplus(float v) { return v > 20.f ? v : log1pf(expf(v)); }
+__device__ inline float front_sigmoid(float v) { return 1.f / (1.f + expf(-v)); }
+
+template <typename T, int V>
+__global__ __launch_bounds__(kThreads) void ssm_front_kernel(const T* __restrict__ dt,
+                                                             const T* __restrict__ g,
+                                                             const T* __restrict__ x,
+                                                             T* __restrict__ delta,
+                                                             T* __restrict__ s, int64_t n_vec) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_vec; i += stride) {
+    float a[V], b[V], c[V], od[V], os[V];
+    if constexpr (V == 1) {
+      a[0] = load_scalar(dt + i);
+      b[0] = load_scalar(g + i);
+      c[0] = load_scalar(x + i);
+    } else {
+      load_vec<T, V>(dt + i * V, a);
+      load_vec<T, V>(g + i * V, b);
+      load_vec<T, V>(x + i * V, c);
+    }
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      od[e] = front_softplus(a[e]);
+      os[e] = front_sigmoid(b[e]) * c[e];
+    }
+    if constexpr (V == 1) {
+      store_scalar(delta + i, od[0]);
+      store_scalar(s + i, os[0]);
+    } else {
+      store_vec<T, V>(delta + i * V, od);
+      store_vec<T, V>(s + i * V, os);
+    }
+  }
+}
+
+template <typename T, int V>
+__global__ __launch_bounds__(kThreads) void ssm_front_bwd_kernel(
+    const T* __restrict__ dt, const T* __restrict__ g, const T* __restrict__ x,
+    const float* __restrict__ dd, const float* __restrict__ ds, T* __restrict__ ddt,
+    T* __restrict__ dg, T* __restrict__ dx, int64_t n_vec) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_vec; i += stride) {
+    float a[V], b[V], c[V], gd[V], gs[V], o1[V], o2[V], o3[V];
+    if constexpr (V == 1) {
+      a[0] = load_scalar(dt + i);
+      b[0] = load_scalar(g + i);
+      c[0] = load_scalar(x + i);
+      gd[0] = dd[i];
+      gs[0] = ds[i];
+    } else {
+      load_vec<T, V>(dt + i * V, a);
+      load_vec<T, V>(g + i * V, b);
+      load_vec<T, V>(x + i * V, c);
+      load_vec<float, V>(dd + i * V, gd);
+      load_vec<float, V>(ds + i * V, gs);
+    }
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      o1[e] = a[e] > 20.f ? gd[e] : gd[e] * front_sigmoid(a[e]);
+      const float sg = front_sigmoid(b[e]);
+      o2[e] = gs[e] * c[e] * sg * (1.f - sg);
+      o3[e] = gs[e] * sg;
+    }
+    if constexpr (V == 1) {
+      store_scalar(ddt + i, o1[0]);
+      store_scalar(dg + i, o2[0]);
+      store_scalar(dx + i, o3[0]);
+    } else {
+      store_vec<T, V>(ddt + i * V, o1);
+      store_vec<T, V>(dg + i * V, o2);
+      store_vec<T, V>(dx + i * V, o3);
+    }
+  }
+}
+
+template <typename T>
+int launch_ssm_front(const void* dt, const void* g, const void* x, void* delta, void* s,
+                     int64_t n, hipStream_t st) {
+  if (n == 0) return MQC_OK;
+  constexpr int V = 16 / sizeof(T);
+  if (n % V == 0 && aligned(dt, 16) && aligned(g, 16) && aligned(x, 16) && aligned(delta, 16) &&
+      aligned(s, 16)) {
+    ssm_front_kernel<T, V><<<dim3((unsigned)grid_for(n / V, kThreads)), dim3(kThreads), 0, st>>>(
+        (const T*)dt, (const T*)g, (const T*)x, (T*)delta, (T*)s, n / V);
+  } else {
+    if (!aligned(dt, sizeof(T)) || !aligned(g, sizeof(T)) || !aligned(x, sizeof(T)) ||
+        !aligned(delta, sizeof(T)) || !aligned(s, sizeof(T)))
+      return MQC_E_ALIGN;
+    ssm_front_kernel<T, 1><<<dim3((unsigned)grid_for(n, kThreads)), dim3(kThreads), 0, st>>>(
+        (const T*)dt, (const T*)g, (const T*)x, (T*)delta, (T*)s, n);
+  }
+  return launch_status();
+}
+
+template <typename T>
+int launch_ssm_front_bwd(const void* dt, const void* g, const void* x, const float* dd,
+                         const float* ds, void* ddt, void* dg, void* dx, int64_t n,
+                         hipStream_t st) {
+  if (n == 0) return MQC_OK;
+  constexpr int V = 16 / sizeof(T);
+  if (n % V == 0 && aligned(dt, 16) && aligned(g, 16) && aligned(x, 16) && aligned(dd, 16) &&
+      aligned(ds, 16) && aligned(ddt, 16) && aligned(dg, 16) && aligned(dx, 16)) {
+    ssm_front_bwd_kernel<T, V><<<dim3((unsigned)grid_for(n / V, kThreads)), dim3(kThreads), 0,
+                                 st>>>((const T*)dt, (const T*)g, (const T*)x, dd, ds, (T*)ddt,
+                                       (T*)dg, (T*)dx, n / V);
+  } else {
+    if (!aligned(dt, sizeof(T)) || !aligned(g, sizeof(T)) || !aligned(x, sizeof(T)) ||
+        !aligned(dd, 4) || !aligned(ds, 4) || !aligned(ddt, sizeof(T)) ||
+        !aligned(dg, sizeof(T)) || !aligned(dx, sizeof(T)))
+      return MQC_E_ALIGN;
+    ssm_front_bwd_kernel<T, 1><<<dim3((unsigned)grid_for(n, kThreads)), dim3(kThreads), 0,
+                                 st>>>((const T*)dt, (const T*)g, (const T*)x, dd, ds, (T*)ddt,
+                                       (T*)dg, (T*)dx, n);
+  }
+  return launch_status();
+}
+
 }  // namespace mqc
 
 using namespace mqc;
@@ -293,7 +419,7 @@ const char* mqc_status_string(int status) {
   }
 }
 
-int mqc_abi_version(void) { return 2; }
+int mqc_abi_version(void) { return 3; }
 
 int mqc_quaternion_multiply(const void* p, const void* q, void* out, int64_t n_quat, int dtype,
                             void* stream) {
@@ -352,6 +478,37 @@ int mqc_out_gate_fwd(const void* x, const void* z, int64_t z_row_stride, const v
     case MQC_F32: return launch_out_gate<float>(x, z, z_row_stride, y_real, out, rows, cols, s);
     case MQC_BF16: return launch_out_gate<bf16_t>(x, z, z_row_stride, y_real, out, rows, cols, s);
     case MQC_F16: return launch_out_gate<f16_t>(x, z, z_row_stride, y_real, out, rows, cols, s);
+    default: return MQC_E_DTYPE;
+  }
+}
+
+int mqc_ssm_front_fwd(const void* dt_raw, const void* g_raw, const void* x, void* delta, void* s,
+                      int64_t n, int dtype, void* stream) {
+  if (n < 0) return MQC_E_SHAPE;
+  if (n > 0 && (!dt_raw || !g_raw || !x || !delta || !s)) return MQC_E_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case MQC_F32: return launch_ssm_front<float>(dt_raw, g_raw, x, delta, s, n, st);
+    case MQC_BF16: return launch_ssm_front<bf16_t>(dt_raw, g_raw, x, delta, s, n, st);
+    case MQC_F16: return launch_ssm_front<f16_t>(dt_raw, g_raw, x, delta, s, n, st);
+    default: return MQC_E_DTYPE;
+  }
+}
+
+int mqc_ssm_front_bwd(const void* dt_raw, const void* g_raw, const void* x, const float* d_delta,
+                      const float* d_s, void* d_dt_raw, void* d_g_raw, void* d_x, int64_t n,
+                      int dtype, void* stream) {
+  if (n < 0) return MQC_E_SHAPE;
+  if (n > 0 && (!dt_raw || !g_raw || !x || !d_delta || !d_s || !d_dt_raw || !d_g_raw || !d_x))
+    return MQC_E_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case MQC_F32:
+      return launch_ssm_front_bwd<float>(dt_raw, g_raw, x, d_delta, d_s, d_dt_raw, d_g_raw, d_x, n, st);
+    case MQC_BF16:
+      return launch_ssm_front_bwd<bf16_t>(dt_raw, g_raw, x, d_delta, d_s, d_dt_raw, d_g_raw, d_x, n, st);
+    case MQC_F16:
+      return launch_ssm_front_bwd<f16_t>(dt_raw, g_raw, x, d_delta, d_s, d_dt_raw, d_g_raw, d_x, n, st);
     default: return MQC_E_DTYPE;
   }
 }

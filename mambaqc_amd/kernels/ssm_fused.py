@@ -231,3 +231,88 @@ def ssm_forward_fused_dl(delta: torch.Tensor, s: torch.Tensor, B: torch.Tensor,
              y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state, float(eps),
              nat.dtype_code(Bc), nat.stream_of(Bc))
     return (y, h_last) if return_state else y
+
+
+def _front_operands(dt_raw, g_raw, x):
+    if not (dt_raw.shape == g_raw.shape == x.shape):
+        raise ValueError(f"ssm_front: shapes differ {tuple(dt_raw.shape)}, "
+                         f"{tuple(g_raw.shape)}, {tuple(x.shape)}")
+    nat.require_device("ssm_front", dt_raw, g_raw, x)
+    ct = torch.promote_types(torch.promote_types(dt_raw.dtype, g_raw.dtype), x.dtype)
+    return [nat.aligned16(t.detach().to(ct)) for t in (dt_raw, g_raw, x)]
+
+
+def _front_forward(dt, g, xv):
+    delta = torch.empty_like(dt)
+    s = torch.empty_like(dt)
+    nat.call("mqc_ssm_front_fwd", dt, dt.data_ptr(), g.data_ptr(), xv.data_ptr(),
+             delta.data_ptr(), s.data_ptr(), dt.numel(), nat.dtype_code(dt), nat.stream_of(dt))
+    return delta, s
+
+
+def ssm_front(dt_raw: torch.Tensor, g_raw: torch.Tensor, x: torch.Tensor):
+    """delta = softplus(dt_raw), s = sigmoid(g_raw) * x in one HIP pass (inference).
+
+    dt_raw is dt_proj's output and g_raw gate_proj's, as in
+    mambaqc/models/quaternion_mamba2_block.py:183,197-198. The three tensors have
+    one shape; the results come in their promoted dtype (fp32 arithmetic).
+    """
+    return _front_forward(*_front_operands(dt_raw, g_raw, x))
+
+
+def _front_backward(dt, g, xv, d_delta, d_s):
+    d_dt, d_g, d_x = (torch.empty_like(dt) for _ in range(3))
+    d_delta = nat.aligned16(d_delta.float())
+    d_s = nat.aligned16(d_s.float())
+    nat.call("mqc_ssm_front_bwd", dt, dt.data_ptr(), g.data_ptr(), xv.data_ptr(),
+             d_delta.data_ptr(), d_s.data_ptr(), d_dt.data_ptr(), d_g.data_ptr(),
+             d_x.data_ptr(), dt.numel(), nat.dtype_code(dt), nat.stream_of(dt))
+    return d_dt, d_g, d_x
+
+
+class _SsmFrontFusedDL(torch.autograd.Function):
+    """Front (softplus / sigmoid gate) + SSM as one autograd node, so the SSM's
+    fp32 d_delta and d_s reach the front's backward without a round trip
+    through the (possibly fp16) dtype of delta and s."""
+
+    @staticmethod
+    def forward(ctx, dt_raw, g_raw, x, B, C, lambda_alpha, lambda_imag, D, h0, eps):
+        dt, g, xv = _front_operands(dt_raw, g_raw, x)
+        delta, s = _front_forward(dt, g, xv)
+        y, h_last, saved = ssm_fused_dl_train_forward(delta, s, B, C, lambda_alpha,
+                                                      lambda_imag, D, h0, eps)
+        del delta, s
+        ctx.save_for_backward(dt, g, xv, *[t for t in saved if t is not None])
+        ctx.has_h0 = h0 is not None
+        ctx.meta = (eps, dt_raw.dtype, g_raw.dtype, x.dtype, lambda_alpha.dtype,
+                    lambda_imag.dtype, D.dtype, None if h0 is None else h0.dtype)
+        return y, h_last
+
+    @staticmethod
+    def backward(ctx, gy, gh_last):
+        dt, g, xv, *saved = ctx.saved_tensors
+        if not ctx.has_h0:
+            saved.insert(7, None)
+        eps, t_dt, t_g, t_x, t_la, t_li, t_D, t_h0 = ctx.meta
+        d_delta, d_s, dB, dC, dla, dli, dD, dh0 = ssm_fused_dl_backward(saved, gy, gh_last, eps)
+        d_dt, d_g, d_x = _front_backward(dt, g, xv, d_delta, d_s)
+        return (d_dt.to(t_dt), d_g.to(t_g), d_x.to(t_x), dB, dC, dla.to(t_la), dli.to(t_li),
+                dD.to(t_D), None if dh0 is None else dh0.to(t_h0), None)
+
+
+def ssm_forward_front_dl(dt_raw: torch.Tensor, g_raw: torch.Tensor, x: torch.Tensor,
+                         B: torch.Tensor, C: torch.Tensor, lambda_alpha: torch.Tensor,
+                         lambda_imag: torch.Tensor, D: torch.Tensor, eps: float = 1e-6,
+                         h0: torch.Tensor | None = None, return_state: bool = False):
+    """The block's whole SSM from the projections' outputs: delta =
+    softplus(dt_raw), s = sigmoid(g_raw) * x, then ssm_forward_fused_dl.
+    Differentiable in every tensor argument when autograd is recording."""
+    inputs = (dt_raw, g_raw, x, B, C, lambda_alpha, lambda_imag, D) + (
+        (h0,) if h0 is not None else ())
+    if torch.is_grad_enabled() and any(t.requires_grad for t in inputs):
+        y, h_last = _SsmFrontFusedDL.apply(dt_raw, g_raw, x, B, C, lambda_alpha, lambda_imag,
+                                           D, h0, eps)
+        return (y, h_last) if return_state else y
+    delta, s = ssm_front(dt_raw, g_raw, x)
+    return ssm_forward_fused_dl(delta, s, B, C, lambda_alpha, lambda_imag, D, eps=eps, h0=h0,
+                                return_state=return_state)

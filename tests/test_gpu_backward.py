@@ -67,6 +67,42 @@ def test_ssm_dl_backward(shape, dtype):
         assert_close(a.grad, r.grad, tol(dtype), f"{name} {shape} {dtype}")
 
 
+@pytest.mark.parametrize("shape", [(2, 37, 5, 16), (1, 9, 13, 3), (2, 16, 8, 64)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_ssm_front_backward(shape, dtype):
+    """Front (delta = softplus(dt_raw), s = sigmoid(g_raw) * x) + SSM as one
+    autograd node, against torch autograd of the same composition on the
+    oracle in float64. dt_raw has entries above softplus' threshold (20)."""
+    b, T, d, k = shape
+    ins = _dl_inputs(b, T, d, k, seed=sum(shape) + 1, dtype=dtype)
+    g = torch.Generator().manual_seed(11)
+    dt = (torch.randn(b, T, d, generator=g) - 1).to(dtype)
+    dt[0, 0, 0] = 22.0
+    gr = (torch.randn(b, T, d, generator=g) * 2).to(dtype)
+    x = torch.randn(b, T, d, generator=g).to(dtype)
+    gy = torch.randn(b, T, d, 4, generator=g).to(dtype)
+    h0 = (torch.randn(b, d, k, 4, generator=g) * 0.5).to(dtype)
+    rest = ins[2:]
+
+    got_in = [_leaf(t, DEV) for t in [dt, gr, x] + rest + [h0]]
+    y = K.ssm_forward_front_dl(*got_in[:8], h0=got_in[8])
+    (y.float() * gy.to(DEV).float()).sum().backward()
+
+    ref_in = [_leaf(t.double()) for t in [dt, gr, x] + rest + [h0]]
+    delta = torch.nn.functional.softplus(ref_in[0])
+    s = torch.sigmoid(ref_in[1]) * ref_in[2]
+    yr = oracle.ssm_forward_dl_reference(delta, s, *ref_in[3:8], h0=ref_in[8])
+    (yr * gy.double()).sum().backward()
+
+    assert_close(y, yr, tol(dtype), f"y {shape} {dtype}")
+    names = ["d_dt_raw", "d_g_raw", "d_x", "dB", "dC", "dLambda_alpha", "dLambda_imag", "dD",
+             "dh0"]
+    for name, a, r in zip(names, got_in, ref_in):
+        assert a.grad is not None, name
+        assert a.grad.dtype == a.dtype, name
+        assert_close(a.grad, r.grad, tol(dtype), f"{name} {shape} {dtype}")
+
+
 def test_ssm_dl_backward_without_state_terms():
     """No h0 and no gradient on the final state; some steps with a large delta
     (|q| close to 1 - 2/(1 + delta |a|/2)... i.e. strong damping)."""

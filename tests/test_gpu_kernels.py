@@ -229,6 +229,44 @@ def test_ssm_fused_dl(shape, dtype):
     assert_close(got, want, tol(dtype), f"ssm_dl {shape} {dtype}")
 
 
+@pytest.mark.parametrize("shape", [(2, 37, 48), (1, 5, 3), (3, 1, 1), (4, 64, 1536)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_ssm_front(shape, dtype):
+    """delta = softplus(dt_raw), s = sigmoid(g_raw) * x against float64 torch on
+    the same rounded inputs; dt_raw spans torch's softplus threshold (20), and
+    known answers pin softplus(0) = log 2, softplus(25) = 25 and s = x / 2 at
+    g_raw = 0."""
+    g = torch.Generator().manual_seed(sum(shape))
+    dt = (torch.randn(*shape, generator=g) * 8).to(dtype)
+    gr = (torch.randn(*shape, generator=g) * 4).to(dtype)
+    x = torch.randn(*shape, generator=g).to(dtype)
+    flat_dt, flat_g = dt.view(-1), gr.view(-1)
+    flat_dt[0] = 0.0
+    flat_g[0] = 0.0
+    if flat_dt.numel() > 2:
+        flat_dt[1], flat_dt[2] = 25.0, -30.0
+    delta, sv = K.ssm_front(dt.to(DEV), gr.to(DEV), x.to(DEV))
+    assert delta.dtype == dtype and sv.dtype == dtype
+    want_d = torch.nn.functional.softplus(dt.double())
+    want_s = torch.sigmoid(gr.double()) * x.double()
+    assert_close(delta, want_d, tol(dtype), f"delta {shape} {dtype}")
+    assert_close(sv, want_s, tol(dtype), f"s {shape} {dtype}")
+    r = 1e-6 if dtype == torch.float32 else 4e-3
+    assert abs(delta.view(-1)[0].item() - np.log(2.0)) <= r
+    assert abs(sv.view(-1)[0].item() - x.view(-1)[0].item() / 2) <= r * (1 + abs(x.view(-1)[0].item()))
+    if flat_dt.numel() > 2:
+        assert delta.view(-1)[1].item() == 25.0
+
+
+def test_ssm_front_unaligned_views():
+    """Odd-offset views take the element-wise path and give the same values."""
+    base = torch.randn(3, 1 + 2 * 5 * 7, device=DEV)
+    dt, gr, x = (base[i, 1:].view(2, 5, 7) for i in range(3))
+    d1, s1 = K.ssm_front(dt, gr, x)
+    d2, s2 = K.ssm_front(dt.contiguous(), gr.contiguous(), x.contiguous())
+    assert torch.equal(d1, d2) and torch.equal(s1, s2)
+
+
 def test_ssm_fused_dl_state_carry():
     """Running [0, T) equals running [0, t1) then [t1, T) from the carried state."""
     a = _dl_inputs(2, 40, 6, 64, seed=41, dtype=torch.float32)

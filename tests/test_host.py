@@ -29,7 +29,7 @@ def declared_symbols():
 
 def test_header_declares_the_api():
     names = declared_symbols()
-    assert len(names) == 20, names
+    assert len(names) == 22, names
     assert set(nat.SIGNATURES) <= set(names)
 
 
@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     lib = nat.load()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mqc_abi_version() == nat.ABI_VERSION == 2
+    assert lib.mqc_abi_version() == nat.ABI_VERSION == 3
 
 
 def test_status_strings():
@@ -68,7 +68,16 @@ def test_validation_codes_without_gpu():
     assert lib.mqc_qln_fwd(FAKE, FAKE, FAKE, FAKE, None, None, 3, 0, 1e-5, 0, None) == -2
     # Gate row stride shorter than the row.
     assert lib.mqc_out_gate_fwd(FAKE, FAKE, 4, FAKE, FAKE, 2, 8, 0, None) == -2
+    # Front of the SSM: negative size, missing output, unknown dtype, misaligned.
+    assert lib.mqc_ssm_front_fwd(FAKE, FAKE, FAKE, FAKE, FAKE, -1, 0, None) == -2
+    assert lib.mqc_ssm_front_fwd(FAKE, FAKE, FAKE, FAKE, None, 8, 0, None) == -1
+    assert lib.mqc_ssm_front_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 8, 4,
+                                 None) == -3
+    assert lib.mqc_ssm_front_fwd(ctypes.c_void_p(4097), FAKE, FAKE, FAKE, FAKE, 3, 1,
+                                 None) == -4
     # Nothing to do is not an error.
+    assert lib.mqc_ssm_front_bwd(None, None, None, None, None, None, None, None, 0, 1,
+                                 None) == 0
     assert lib.mqc_quaternion_multiply(None, None, None, 0, 0, None) == 0
     assert lib.mqc_cumprod_scan_fwd(None, None, 0, 5, 5, 0, None) == 0
 
