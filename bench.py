@@ -365,6 +365,9 @@ def train_timings(args):
     x = torch.randn(B, T, DM, generator=g, device="cuda")
 
     def step():
+        # As the reference's training step (train.py:206): gradients set to None,
+        # so each backward writes them fresh instead of accumulating.
+        blk.zero_grad(set_to_none=True)
         with torch.autocast("cuda", dtype=torch.float16):
             loss = blk(x).float().pow(2).mean()
         (loss * 2.0 ** 16).backward()

@@ -56,16 +56,15 @@ struct SsmBwdArgs {
 // Pull dq back through q = Cayley(dl * Lambda) (closed form, see ssm_scan.hpp):
 //   N = 1 - dl a + dl^2 n2 (clamped below at eps), P = 1 - dl^2 n2,
 //   q0 = P / N,  qv = dl v / N.
+// r = 1 / max(N, eps) and live = (N > eps) come from the state recompute.
 // Returns d dl; accumulates the gradients w.r.t. a and v into da, dv. When the
 // clamp engages N is constant, as in the reference's clamp_min.
 __device__ inline float cayley_pullback(const quat& g, const quat& q, float dl, float dl2,
-                                        const LamConst& L, float eps, float& da, float (&dv)[3]) {
-  const float Nraw = fmaf(dl2, L.n2, fmaf(-dl, L.a, 1.f));
-  const float live = Nraw > eps ? 1.f : 0.f;
-  const float r = __builtin_amdgcn_rcpf(fmaxf(Nraw, eps));
+                                        float r, bool live, const LamConst& L, float& da,
+                                        float (&dv)[3]) {
   const float gq = g.w * q.w + g.x * q.x + g.y * q.y + g.z * q.z;   // <dq, q>
   const float gv = g.x * L.v0 + g.y * L.v1 + g.z * L.v2;            // <dq_vec, v>
-  const float gql = gq * live;
+  const float gql = live ? gq : 0.f;
   // d/d dl: dP = -2 dl n2, dN = -a + 2 dl n2
   const float ddl = (g.w * (-2.f * dl * L.n2) + gv - gql * fmaf(2.f * dl, L.n2, -L.a)) * r;
   // d/da: dP = -dl^2 a / 2, dN = -dl + dl^2 a / 2
@@ -112,12 +111,15 @@ __device__ inline void group_reduce2(float& u, float& w, int lane) {
 
 // SYNC: a block barrier after every chunk keeps the block's waves on the same
 // chunk. Unlike the forward, the backward gains nothing from it: it is VALU
-// bound (about 220 VALU instructions per step and lane, 4.6 ms of issue at
-// config 3 against 5 ms of HBM traffic), so the launcher runs free 256-thread
+// bound (about 215 VALU instructions per step and lane at bf16 and G = 64,
+// against 5 ms of HBM traffic at config 3), so the launcher runs free 256-thread
 // blocks, measured 4 % faster than lockstep 768-thread ones. Double-buffering
 // the chunk operands was measured too and gave nothing at K = 8.
-template <typename T, int G, int K, int NT, bool FULL, bool SYNC>
-__global__ __launch_bounds__(NT) void ssm_bwd_kernel(SsmBwdArgs a) {
+// WPE caps the registers at two waves per SIMD (<= 256 VGPRs): left alone the
+// compiler takes 276 (one wave per SIMD); at three waves per SIMD it spills to
+// scratch and runs twice as slow.
+template <typename T, int G, int K, int NT, bool FULL, bool SYNC, int WPE = 2>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void ssm_bwd_kernel(SsmBwdArgs a) {
   static_assert((G & (G - 1)) == 0 && G <= 64 && NT % 64 == 0 && NT % G == 0, "bad group");
   constexpr int GPB = NT / G;
   const int tid = threadIdx.x;
@@ -154,33 +156,50 @@ __global__ __launch_bounds__(NT) void ssm_bwd_kernel(SsmBwdArgs a) {
   }
 
   // Operands of one chunk: the K steps' delta, s, B, C, gy (raw bits) and the
-  // checkpointed state before the chunk.
+  // checkpointed state before the chunk. Addresses are a chunk base (uniform)
+  // plus a 32-bit per-lane offset; the launcher checks that K steps of every
+  // tensor fit in 32 bits.
   struct Ops {
     Raw<T, 1> rd[K], rs[K];
     Raw<T, 4> rB[K], rC[K], rg[K];
     float4 h_in;
   };
-  auto load_chunk = [&](Ops& o, int64_t c) {
-    const int64_t t0 = c * K;
-    const int len = (int)(Tn - t0 < K ? Tn - t0 : K);
+  const uint32_t stepBC = (uint32_t)(rowBC * (int64_t)sizeof(T));
+  const uint32_t stepTok = (uint32_t)(rowTok * (int64_t)sizeof(T));
+  const uint32_t stepY = (uint32_t)(rowY * (int64_t)sizeof(T));
+  const uint32_t stepF = (uint32_t)(rowTok * 4);  // fp32 d_delta, d_s
+  const uint32_t offF = (uint32_t)(d * 4);
+  auto load_chunk = [&](Ops& o, int64_t c, int len) {
+    const int64_t row0 = b * Tn + c * K;
+    const char* pD = (const char*)a.delta + row0 * stepTok;
+    const char* pS = (const char*)a.s + row0 * stepTok;
+    const char* pB = (const char*)a.Bm + row0 * (int64_t)stepBC;
+    const char* pC = (const char*)a.Cm + row0 * (int64_t)stepBC;
+    const char* pG = (const char*)a.gy + row0 * (int64_t)stepY;
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-      // The tail chunk re-reads its last step.
-      const int64_t rt = b * Tn + t0 + (i < len ? i : len - 1);
-      raw_load<T, 1>((const char*)((const T*)a.delta + rt * rowTok) + offTok, o.rd[i]);
-      raw_load<T, 1>((const char*)((const T*)a.s + rt * rowTok) + offTok, o.rs[i]);
-      raw_load<T, 4>((const char*)((const T*)a.Bm + rt * rowBC) + offBC, o.rB[i]);
-      raw_load<T, 4>((const char*)((const T*)a.Cm + rt * rowBC) + offBC, o.rC[i]);
-      raw_load<T, 4>((const char*)((const T*)a.gy + rt * rowY) + offY, o.rg[i]);
+      // A tail chunk re-reads its last step.
+      const uint32_t ii = (uint32_t)(i < len ? i : len - 1);
+      raw_load<T, 1>(pD + ii * (int64_t)stepTok + offTok, o.rd[i]);
+      raw_load<T, 1>(pS + ii * (int64_t)stepTok + offTok, o.rs[i]);
+      raw_load<T, 4>(pB + ii * (int64_t)stepBC + offBC, o.rB[i]);
+      raw_load<T, 4>(pC + ii * (int64_t)stepBC + offBC, o.rC[i]);
+      raw_load<T, 4>(pG + ii * (int64_t)stepY + offY, o.rg[i]);
     }
     // The checkpoint of the previous chunk (chunk 0 starts from h0, read in process).
     const int64_t cp = c > 0 ? c - 1 : 0;
     o.h_in = *reinterpret_cast<const float4*>(a.h_ckpt + (((b * nC + cp) * a.Dm + d) * a.S + k) * 4);
   };
-  auto process_chunk = [&](Ops& o, int64_t c) {
-    const int64_t t0 = c * K;
-    const int len = (int)(Tn - t0 < K ? Tn - t0 : K);
+  // FULLC: all K steps of the chunk exist (every chunk but a ragged last one).
+  auto process_chunk = [&](auto fullc, Ops& o, int64_t c, int len) {
+    constexpr bool FULLC = decltype(fullc)::value;
+    const int64_t row0 = b * Tn + c * K;
+    char* pdB = (char*)a.dB + row0 * (int64_t)stepBC;
+    char* pdC = (char*)a.dC + row0 * (int64_t)stepBC;
+    char* pdd = (char*)a.d_delta + row0 * (int64_t)stepF;
+    char* pds = (char*)a.d_s + row0 * (int64_t)stepF;
     quat hs[K + 1];
+    float rq[K];  // 1 / max(N, eps) of each step, negated where the clamp engaged
     if (c > 0) {
       hs[0] = quat{o.h_in.x, o.h_in.y, o.h_in.z, o.h_in.w};
     } else if (a.h0) {
@@ -190,24 +209,30 @@ __global__ __launch_bounds__(NT) void ssm_bwd_kernel(SsmBwdArgs a) {
     } else {
       hs[0] = quat{0.f, 0.f, 0.f, 0.f};
     }
-    // Recompute the chunk's states.
+    // Recompute the chunk's states (the forward's arithmetic).
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-      if (i < len) {
+      if (FULLC || i < len) {
         const float dl = raw_get(o.rd[i], 0);
-        const quat q = cayley_step(dl, dl * dl, L, a.eps);
+        const float dl2 = dl * dl;
+        const float Nraw = fmaf(dl2, L.n2, fmaf(-dl, L.a, 1.f));
+        const float r = __builtin_amdgcn_rcpf(fmaxf(Nraw, a.eps));
+        rq[i] = Nraw > a.eps ? r : -r;
+        const float cq = dl * r;
+        const quat q{fmaf(-dl2, L.n2, 1.f) * r, cq * L.v0, cq * L.v1, cq * L.v2};
         hs[i + 1] = state_step(q, hs[i], raw_get(o.rs[i], 0), raw_quat(o.rB[i], 0));
       }
     }
     // Adjoint steps, last to first.
 #pragma unroll
     for (int i = K - 1; i >= 0; --i) {
-      if (i < len) {
-        const int64_t rt = b * Tn + t0 + i;
+      if (FULLC || i < len) {
         const float dl = raw_get(o.rd[i], 0);
         const float dl2 = dl * dl;
         const float sv = raw_get(o.rs[i], 0);
-        const quat q = cayley_step(dl, dl2, L, a.eps);
+        const float r = fabsf(rq[i]);
+        const float cq = dl * r;
+        const quat q{fmaf(-dl2, L.n2, 1.f) * r, cq * L.v0, cq * L.v1, cq * L.v2};
         const quat gy = raw_quat(o.rg[i], 0);
         const quat Ck = raw_quat(o.rC[i], 0);
         const quat Bk = raw_quat(o.rB[i], 0);
@@ -217,24 +242,24 @@ __global__ __launch_bounds__(NT) void ssm_bwd_kernel(SsmBwdArgs a) {
         qmul_acc(dq, g, qconj(hs[i]));
         quat dC{0.f, 0.f, 0.f, 0.f};
         qmul_acc(dC, gy, qconj(hs[i + 1]));
-        float ddl = cayley_pullback(dq, q, dl, dl2, L, a.eps, da, dv);
+        float ddl = cayley_pullback(dq, q, dl, dl2, r, rq[i] > 0.f, L, da, dv);
         float dsk = g.w * Bk.w + g.x * Bk.x + g.y * Bk.y + g.z * Bk.z;
         carry = quat{0.f, 0.f, 0.f, 0.f};
         qmul_acc(carry, qconj(q), g);
         if (own) {
           const float eB[4] = {sv * g.w, sv * g.x, sv * g.y, sv * g.z};
           const float eC[4] = {dC.w, dC.x, dC.y, dC.z};
-          store_vec<T, 4>((T*)a.dB + rt * rowBC + (d * a.S + k) * 4, eB);
-          store_vec<T, 4>((T*)a.dC + rt * rowBC + (d * a.S + k) * 4, eC);
+          store_vec<T, 4>((T*)(pdB + i * (int64_t)stepBC + offBC), eB);
+          store_vec<T, 4>((T*)(pdC + i * (int64_t)stepBC + offBC), eC);
         } else {
           ddl = 0.f;
           dsk = 0.f;
         }
         group_reduce2<G>(ddl, dsk, lane);
         if (gvalid) {
-          if (j == 0) a.d_delta[rt * rowTok + d] = ddl;
+          if (j == 0) *(float*)(pdd + i * (int64_t)stepF + offF) = ddl;
           if (j == (G > 1 ? 1 : 0)) {
-            a.d_s[rt * rowTok + d] = fmaf(Dv, gy.w, dsk);
+            *(float*)(pds + i * (int64_t)stepF + offF) = fmaf(Dv, gy.w, dsk);
             dD = fmaf(gy.w, sv, dD);
           }
         }
@@ -244,9 +269,18 @@ __global__ __launch_bounds__(NT) void ssm_bwd_kernel(SsmBwdArgs a) {
   };
 
   Ops buf;
-  for (int64_t c = nC - 1; c >= 0; --c) {
-    load_chunk(buf, c);
-    process_chunk(buf, c);
+  {
+    const int64_t c = nC - 1;
+    const int len = (int)(Tn - c * K);
+    load_chunk(buf, c, len);
+    if (len == K)
+      process_chunk(std::integral_constant<bool, true>{}, buf, c, len);
+    else
+      process_chunk(std::integral_constant<bool, false>{}, buf, c, len);
+  }
+  for (int64_t c = nC - 2; c >= 0; --c) {
+    load_chunk(buf, c, K);
+    process_chunk(std::integral_constant<bool, true>{}, buf, c, K);
   }
 
   if (own) {
@@ -289,7 +323,9 @@ int launch_ssm_bwd_g(const SsmBwdArgs& a, hipStream_t s) {
 template <typename T>
 int launch_ssm_bwd(const SsmBwdArgs& a, hipStream_t s) {
   if (a.batch == 0 || a.T == 0 || a.Dm == 0) return MQC_OK;
-  if (a.Dm * a.S * 4 * (int64_t)sizeof(T) >= ((int64_t)1 << 31)) return MQC_E_LIMIT;
+  // K consecutive steps of one tensor must be addressable with 32-bit offsets.
+  if (a.Dm * a.S * 4 * (int64_t)sizeof(T) * ssm_bwd_chunk<T>() >= ((int64_t)1 << 32))
+    return MQC_E_LIMIT;
   const uintptr_t qa = 4 * sizeof(T);
   if (!aligned(a.Bm, qa) || !aligned(a.Cm, qa) || !aligned(a.gy, qa) || !aligned(a.dB, qa) ||
       !aligned(a.dC, qa) || !aligned(a.h_ckpt, 16) || (a.h0 && !aligned(a.h0, qa)) ||
