@@ -215,7 +215,7 @@ def read_traffic():
     return None
 
 
-def box_copy_gbs(reps=10):
+def box_copy_gbs(reps=20):
     """Read+write bandwidth of a 1 GiB device-to-device copy on this box. HBM
     throughput differs from box to box by up to ~15 %; this puts the SSM's
     figure beside what a plain copy gets on the same device."""
@@ -223,7 +223,8 @@ def box_copy_gbs(reps=10):
 
     src = torch.empty(1 << 28, device="cuda")
     dst = torch.empty_like(src)
-    dst.copy_(src)
+    for _ in range(3):
+        dst.copy_(src)
     ms = event_time_ms(lambda: dst.copy_(src), reps)
     del src, dst
     torch.cuda.empty_cache()
@@ -235,6 +236,8 @@ def run_full(args):
     from mambaqc_amd import kernels as K
 
     dtype = torch.bfloat16
+    # Measured first, on a cold device, like the standalone copy mode.
+    copy_gbs = box_copy_gbs()
     log(f"building block d_model={DM} d_state={DS} expand={EXPAND} on {torch.cuda.get_device_name(0)}")
     blk = make_block(dtype)
     g = torch.Generator(device="cuda").manual_seed(0)
@@ -277,7 +280,6 @@ def run_full(args):
     qln_gbs = qln_bytes(B * T, DI) / (stages["qln"] * 1e-3) / 1e9
     del delta, s, Bq, Cq
     torch.cuda.empty_cache()
-    copy_gbs = box_copy_gbs()
     log(f"box calibration: 1 GiB device copy {copy_gbs:.0f} GB/s; fused SSM at "
         f"{achieved / copy_gbs:.1%} of it")
 
@@ -297,8 +299,8 @@ def run_full(args):
     del z, q
     torch.cuda.empty_cache()
 
-    train = train_timings(args)
-    lm = lm_timing(args)
+    train = None if args.block_only else train_timings(args)
+    lm = None if args.block_only else lm_timing(args)
 
     base = None if args.no_cpu else cpu_baseline(blk, x)
     if base:
@@ -537,6 +539,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--mode", default="full")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--block-only", action="store_true",
+                    help="skip the config-4 and config-5 legs (for a kernel trace of the block)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's hot path runs on a single MI355X "
