@@ -510,9 +510,9 @@ def run_kernel_loop(args):
             # one step per token through every block (bf16, batch 4).
             import mambaqc_amd
             torch.manual_seed(0)
-            with torch.device("cuda"):
-                lm = mambaqc_amd.quaternion_mamba2_base(10000)
-            lm = lm.to(torch.bfloat16).eval()
+            # Parameters built outside inference mode, as in lm_timing.
+            with torch.inference_mode(False), torch.device("cuda"):
+                lm = mambaqc_amd.quaternion_mamba2_base(10000).to(torch.bfloat16).eval()
             ids = torch.randint(0, 10000, (B, 64), generator=g, device="cuda")
             _, states = lm.forward_with_state(ids)
             tok = ids[:, -1:]

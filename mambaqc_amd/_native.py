@@ -11,6 +11,7 @@ device pointers handed across are then valid on both sides.
 from __future__ import annotations
 
 import ctypes
+import weakref
 import os
 import threading
 from pathlib import Path
@@ -138,6 +139,34 @@ def aligned16(t: torch.Tensor) -> torch.Tensor:
     if t.data_ptr() % 16 != 0:
         t = t.clone()
     return t
+
+
+# Converted copies of parameters by id(), dropped when the parameter object
+# dies (kept off the tensor itself so that pickling a module does not carry them).
+_F32_CACHE: dict = {}
+
+
+def param_f32(t: torch.Tensor) -> torch.Tensor:
+    """fp32, contiguous, 16-byte aligned form of a parameter-like tensor (the
+    kernels read Lambda, D, gamma, beta and conv weights in fp32 whatever the
+    model dtype). An fp32 tensor that already qualifies is used as is; other
+    conversions are cached and redone when the tensor's data pointer, shape or
+    version counter (bumped by every in-place update) changes. Inference
+    tensors have no version counter and are converted on every call."""
+    if t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0:
+        return t.detach()
+    if t.is_inference():
+        # No version counter to tell an in-place update: convert every time.
+        return aligned16(t.detach().float())
+    key = (t._version, t.data_ptr(), t.dtype, tuple(t.shape))
+    hit = _F32_CACHE.get(id(t))
+    if hit is not None and hit[0]() is t and hit[1] == key:
+        return hit[2]
+    conv = aligned16(t.detach().float())
+    if hit is None or hit[0]() is not t:
+        weakref.finalize(t, _F32_CACHE.pop, id(t), None)
+    _F32_CACHE[id(t)] = (weakref.ref(t), key, conv)
+    return conv
 
 
 def call(name: str, device_tensor: torch.Tensor, *args) -> None:

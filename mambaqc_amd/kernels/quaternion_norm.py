@@ -17,8 +17,8 @@ from .. import _native as nat
 def _qln_forward(q, gamma, beta, eps, want_stats):
     B, T, D, _ = q.shape
     q = nat.aligned16(q.detach())
-    g = nat.aligned16(gamma.detach().float())
-    b = nat.aligned16(beta.detach().float())
+    g = nat.param_f32(gamma)
+    b = nat.param_f32(beta)
     out = torch.empty_like(q)
     mean = rstd = None
     if want_stats:

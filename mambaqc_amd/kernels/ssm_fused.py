@@ -113,7 +113,7 @@ def _dl_operands(delta, s, B, C, lambda_alpha, lambda_imag, D, h0):
     dtype = B.dtype
     ops = [nat.aligned16(t.detach().to(dtype)) for t in (delta, s)]
     ops += [nat.aligned16(t.detach()) for t in (B, C)]
-    ops += [nat.aligned16(t.detach().float()) for t in (lambda_alpha, lambda_imag, D)]
+    ops += [nat.param_f32(t) for t in (lambda_alpha, lambda_imag, D)]
     ops.append(None if h0 is None else nat.aligned16(h0.detach().to(dtype)))
     return ops
 

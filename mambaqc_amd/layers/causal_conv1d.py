@@ -57,8 +57,8 @@ class _ConvSiLU(torch.autograd.Function):
         B, T, C = x.shape
         K = weight.shape[-1]
         xv, xs = _rows_view(x.detach())
-        w = weight.detach().float().reshape(C, K).contiguous()
-        b = None if bias is None else bias.detach().float().contiguous()
+        w = nat.param_f32(weight).reshape(C, K)
+        b = None if bias is None else nat.param_f32(bias)
         out = torch.empty(B, T, C, device=x.device, dtype=x.dtype)
         nat.call("mqc_causal_conv_silu_fwd", xv, xv.data_ptr(), xs, w.data_ptr(), nat.ptr(b),
                  out.data_ptr(), B, T, C, K, nat.dtype_code(xv), nat.stream_of(xv))

@@ -390,6 +390,23 @@ def test_block_bf16_vs_oracle():
     assert_close(got, want, 2e-2, "block bf16")
 
 
+def test_block_built_under_inference_mode():
+    """A bf16 block whose parameters are inference tensors (built inside
+    torch.inference_mode) gives the same output as one built normally; its
+    parameter conversions cannot be cached and are redone every call."""
+    torch.manual_seed(3)
+    ref_blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=16).to(DEV, torch.bfloat16)
+    x = torch.randn(2, 20, 64, device=DEV).to(torch.bfloat16)
+    with torch.inference_mode():
+        torch.manual_seed(3)
+        blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=16).to(DEV, torch.bfloat16)
+        assert blk.Lambda_alpha.is_inference()
+        got = blk(x)
+        got2 = blk(x)
+        want = ref_blk(x)
+    assert torch.equal(got, want) and torch.equal(got2, want)
+
+
 # ---------------------------------------------------------------- front of block
 def _conv_silu_ref(x, w, b):
     """silu(CausalConv1d(x)) in float64 (layers/causal_conv1d.py:68-91 + F.silu)."""

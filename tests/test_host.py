@@ -193,3 +193,27 @@ def test_lm_presets_shapes():
     n = sum(p.numel() for p in base.parameters())
     assert base.vocab_size_padded == 10000 and len(base.layers) == 12
     assert 14.6e9 < n < 14.7e9, n  # the B/C projections dominate
+
+
+def test_param_f32_cache():
+    """fp32 copies of parameters are reused while the parameter is unchanged,
+    redone after an in-place update, skipped for fp32 parameters, and dropped
+    with the parameter."""
+    import gc
+    p = torch.nn.Parameter(torch.randn(5, 3).bfloat16())
+    a = nat.param_f32(p)
+    assert a.dtype == torch.float32 and nat.param_f32(p) is a
+    with torch.no_grad():
+        p.add_(1)
+    b = nat.param_f32(p)
+    assert b is not a and torch.equal(b, p.detach().float())
+    q = torch.nn.Parameter(torch.randn(4, 4))
+    assert nat.param_f32(q).data_ptr() == q.data_ptr()
+    key = id(p)
+    assert key in nat._F32_CACHE
+    del p, a, b
+    gc.collect()
+    assert key not in nat._F32_CACHE
+    with torch.inference_mode():
+        r = torch.randn(3, 2).bfloat16()
+        assert torch.equal(nat.param_f32(r), r.float())
