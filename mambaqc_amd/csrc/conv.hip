@@ -30,7 +30,9 @@ constexpr int kConvMaxK = 8;
 template <typename T>
 constexpr int conv_vec() { return 16 / (int)sizeof(T); }
 
-__device__ inline float sigmoid_f(float x) { return 1.f / (1.f + __expf(-x)); }
+// Hardware exp and reciprocal (about 1 ulp each); the IEEE division would
+// cost ten instructions per element in what is otherwise a few FMAs.
+__device__ inline float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 // V consecutive elements: one 16-byte access, or V == 1 (any alignment).
 template <typename T, int V>
@@ -204,7 +206,13 @@ __global__ __launch_bounds__(kConvThreads) void conv_silu_bwd_kernel(
   }
 }
 
-constexpr int kConvRun = 16;  // steps per thread
+constexpr int kConvRun = 16;  // steps per thread (the backward's partial sums come per run)
+constexpr int kConvRunShort = 4;
+// Forward threads below which the short run is used: 4 waves per SIMD of the
+// 256 CUs. Short runs re-read K-1 rows per run (from L2) but give the small
+// launches (decoding, short prompts, config 3's 98 304 long runs) more waves
+// to hide latency with.
+constexpr int64_t kConvShortBelow = 256LL * 4 * 4 * 64;
 
 template <typename T, int K, int V>
 int launch_conv_kv(bool bwd, const void* x, int64_t xs, const float* w, const float* bias,
@@ -214,7 +222,13 @@ int launch_conv_kv(bool bwd, const void* x, int64_t xs, const float* w, const fl
   const int64_t items = Bn * runs * (C / V);
   const int64_t blocks = (items + kConvThreads - 1) / kConvThreads;
   if (blocks > 0x7fffffffLL) return MQC_E_LIMIT;
-  if (!bwd)
+  if (!bwd && items < kConvShortBelow) {
+    const int64_t items_s = Bn * ((T_len + kConvRunShort - 1) / kConvRunShort) * (C / V);
+    const int64_t blocks_s = (items_s + kConvThreads - 1) / kConvThreads;
+    conv_silu_fwd_kernel<T, K, kConvRunShort, V><<<dim3((unsigned)blocks_s), dim3(kConvThreads),
+                                                   0, s>>>((const T*)x, xs, w, bias,
+                                                           (T*)out_or_dx, Bn, T_len, C);
+  } else if (!bwd)
     conv_silu_fwd_kernel<T, K, kConvRun, V><<<dim3((unsigned)blocks), dim3(kConvThreads), 0, s>>>(
         (const T*)x, xs, w, bias, (T*)out_or_dx, Bn, T_len, C);
   else

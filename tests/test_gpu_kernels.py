@@ -430,3 +430,21 @@ def test_causal_conv_silu(shape, dtype):
     got = causal_conv1d_silu(x_in, w.to(DEV), bias.to(DEV))
     assert got.is_contiguous() and got.dtype == dtype
     assert_close(got, _conv_silu_ref(xz[..., :C], w, bias), tol(dtype), f"conv_silu {shape} {dtype}")
+
+
+def test_causal_conv_silu_long_runs():
+    """A launch large enough for 16-step runs per thread (the small shapes above
+    take 4-step runs): B12 T2048 C1536 bf16 against torch's fp32 conv + SiLU on
+    the same rounded input."""
+    from mambaqc_amd.layers.causal_conv1d import causal_conv1d_silu
+    b, T, C, K = 12, 2048, 1536, 4
+    g = torch.Generator(device=DEV).manual_seed(5)
+    xz = torch.randn(b, T, 2 * C, generator=g, device=DEV).to(torch.bfloat16)
+    w = torch.randn(C, 1, K, generator=g, device=DEV) * 0.5
+    bias = torch.randn(C, generator=g, device=DEV) * 0.1
+    x_in = xz.chunk(2, dim=-1)[0]
+    got = causal_conv1d_silu(x_in, w, bias)
+    xt = torch.nn.functional.pad(x_in.float().transpose(1, 2), (K - 1, 0))
+    want = torch.nn.functional.silu(
+        torch.nn.functional.conv1d(xt, w, bias, groups=C)).transpose(1, 2)
+    assert_close(got, want, 2e-2, "conv_silu long runs")
