@@ -448,3 +448,87 @@ def test_causal_conv_silu_long_runs():
     want = torch.nn.functional.silu(
         torch.nn.functional.conv1d(xt, w, bias, groups=C)).transpose(1, 2)
     assert_close(got, want, 2e-2, "conv_silu long runs")
+
+
+# ---------------------------------------------------------------- wide projections
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n", [1000, 4096, 777])
+def test_wide_linear_column_blocks(monkeypatch, dtype, n):
+    """wide_linear's column-block GEMMs (forced here with a 64 KiB weight bound,
+    so N = 777 splits into ragged blocks) equal one fp64 product, and the
+    block's B/C projections take that path under no_grad."""
+    from mambaqc_amd.layers import quaternion_linear as ql
+
+    monkeypatch.setattr(ql, "WIDE_LINEAR_CHUNK_BYTES", 64 << 10)
+    monkeypatch.setattr(ql, "WIDE_LINEAR_MIN_ROWS", 1)
+    x = rnd(3, 5, 96, seed=1, dtype=dtype).to(DEV)
+    w = rnd(n, 96, seed=2, dtype=dtype, scale=0.1).to(DEV)
+    with torch.no_grad():
+        got = ql.wide_linear(x, w)
+    assert got.shape == (3, 5, n) and got.dtype == dtype
+    assert_close(got, up(x) @ up(w).t(), tol(dtype), f"wide_linear {dtype} n={n}")
+
+    lin = ql.real_to_quaternion_projection(96, n // 4 if n % 4 == 0 else 250, bias=True)
+    lin = lin.to(DEV, dtype)
+    with torch.no_grad():
+        lin.bias.normal_()
+        out = lin(x)
+    want = (up(x) @ up(lin.weight).t()).view(3, 5, -1, 4) + up(lin.bias)
+    assert_close(out, want, tol(dtype), f"real->quaternion projection {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_wide_linear_backward(monkeypatch, dtype):
+    """Gradients of the blocked GEMMs (row-block dW, K-block dx with fp32
+    partials) against fp64 products, with ragged blocks."""
+    from mambaqc_amd.layers import quaternion_linear as ql
+
+    monkeypatch.setattr(ql, "WIDE_LINEAR_CHUNK_BYTES", 16 << 10)
+    monkeypatch.setattr(ql, "WIDE_LINEAR_MIN_ROWS", 1)
+    x = rnd(2, 9, 96, seed=5, dtype=dtype).to(DEV).requires_grad_()
+    w = rnd(777, 96, seed=6, dtype=dtype, scale=0.1).to(DEV).requires_grad_()
+    gy = rnd(2, 9, 777, seed=7, dtype=dtype).to(DEV)
+    y = ql.wide_linear(x, w)
+    assert y.grad_fn is not None and len(ql._blocks(777, 96, w.element_size())) > 1
+    y.backward(gy)
+    assert_close(y, up(x) @ up(w).t(), tol(dtype), "y")
+    assert_close(x.grad, up(gy) @ up(w), tol(dtype), "dx")
+    assert_close(w.grad, up(gy).reshape(-1, 777).t() @ up(x).reshape(-1, 96), tol(dtype), "dW")
+
+
+def test_wide_linear_autocast_matches_f_linear(monkeypatch):
+    """Under fp16 autocast the blocked path gives F.linear's dtypes and, within
+    fp16 rounding, its values and gradients (fp32 weight, fp32 input)."""
+    from mambaqc_amd.layers import quaternion_linear as ql
+
+    monkeypatch.setattr(ql, "WIDE_LINEAR_CHUNK_BYTES", 16 << 10)
+    monkeypatch.setattr(ql, "WIDE_LINEAR_MIN_ROWS", 1)
+    x = rnd(3, 7, 64, seed=8).to(DEV)
+    w = rnd(520, 64, seed=9, scale=0.1).to(DEV)
+    outs = []
+    for fn in (ql.wide_linear, torch.nn.functional.linear):
+        xi = x.clone().requires_grad_()
+        wi = w.clone().requires_grad_()
+        with torch.autocast("cuda", dtype=torch.float16):
+            y = fn(xi, wi)
+        assert y.dtype == torch.float16
+        (y.float() ** 2).sum().backward()
+        assert xi.grad.dtype == torch.float32 and wi.grad.dtype == torch.float32
+        outs.append((y, xi.grad, wi.grad))
+    for a, b, what in zip(outs[0], outs[1], ("y", "dx", "dW")):
+        assert_close(a, b, 2e-2, f"autocast {what}")
+
+
+def test_wide_linear_records_autograd(monkeypatch):
+    """With autograd recording, the blocked path records a backward node and
+    its weight gradient is right (fp32, a sum over rows)."""
+    from mambaqc_amd.layers import quaternion_linear as ql
+
+    monkeypatch.setattr(ql, "WIDE_LINEAR_CHUNK_BYTES", 1 << 10)
+    monkeypatch.setattr(ql, "WIDE_LINEAR_MIN_ROWS", 1)
+    x = rnd(4, 32, seed=3).to(DEV).requires_grad_()
+    w = rnd(64, 32, seed=4).to(DEV).requires_grad_()
+    y = ql.wide_linear(x, w)
+    assert y.grad_fn is not None
+    y.sum().backward()
+    assert_close(w.grad, up(x).sum(0, keepdim=True).expand(64, 32), 1e-4, "dW")
