@@ -518,6 +518,21 @@ def run_kernel_loop(args):
             tok = ids[:, -1:]
             fn = lambda: lm.forward_with_state(tok, states)
             nbytes = sum(p.numel() * p.element_size() for p in lm.parameters())
+        elif args.mode == "train":
+            # Config 4: block forward + backward under fp16 autocast, loss
+            # scaled as in train_timings (kernel traces of the training step).
+            torch.manual_seed(0)
+            with torch.inference_mode(False):
+                blk = make_block(torch.float32)
+                x = torch.randn(B, T, DM, generator=g, device="cuda")
+
+            def fn():
+                with torch.inference_mode(False):
+                    blk.zero_grad(set_to_none=True)
+                    with torch.autocast("cuda", dtype=torch.float16):
+                        loss = blk(x).float().pow(2).mean()
+                    (loss * 2.0 ** 16).backward()
+            nbytes = 0
         elif args.mode == "copy":
             src = torch.empty(1 << 28, device="cuda")  # 1 GiB
             dst = torch.empty_like(src)

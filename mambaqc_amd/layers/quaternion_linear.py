@@ -50,37 +50,52 @@ def _wide_forward(x2: torch.Tensor, weight: torch.Tensor, out2: torch.Tensor) ->
 class _WideLinearFunction(torch.autograd.Function):
     """y = x W^T by column blocks; the backward splits the same way:
     dW by row blocks (each dW[n0:n1] = gy[:, n0:n1]^T x, written in place) and
-    dx as a sum over K blocks with fp32 partials, rounded once."""
+    dx as a sum over K blocks with fp32 partials, rounded once.
+
+    `dtype` is the GEMMs' operand dtype (autocast's), or None to use the
+    inputs' own. The casts happen inside the node, so an fp32 weight under
+    16-bit autocast gets its gradient straight from the GEMMs in fp32 (16-bit
+    operands, fp32 accumulation and output) instead of a 16-bit gradient and a
+    separate cast pass over it.
+    """
 
     @staticmethod
-    def forward(ctx, x, weight):
+    def forward(ctx, x, weight, dtype):
         n, k = weight.shape
-        x2 = x.reshape(-1, k)
-        out = torch.empty(*x.shape[:-1], n, device=x.device, dtype=x.dtype)
-        _wide_forward(x2, weight, out.view(-1, n))
-        ctx.save_for_backward(x2, weight)
+        xd = x if dtype is None else x.to(dtype)
+        wd = weight if dtype is None else weight.to(dtype)
+        x2 = xd.reshape(-1, k)
+        out = torch.empty(*x.shape[:-1], n, device=x.device, dtype=wd.dtype)
+        _wide_forward(x2, wd, out.view(-1, n))
+        ctx.save_for_backward(x2, wd)
         ctx.x_shape = x.shape
+        ctx.dtypes = (x.dtype, weight.dtype)
         return out
 
     @staticmethod
     def backward(ctx, gy):
-        x2, weight = ctx.saved_tensors
-        n, k = weight.shape
-        gy2 = gy.reshape(-1, n)
-        blocks = _blocks(n, k, weight.element_size())
+        x2, wd = ctx.saved_tensors
+        x_dtype, w_dtype = ctx.dtypes
+        n, k = wd.shape
+        gy2 = gy.to(wd.dtype).reshape(-1, n)
+        blocks = _blocks(n, k, wd.element_size())
+        wide = {} if wd.dtype == torch.float32 else {"out_dtype": torch.float32}
         dx = dw = None
         if ctx.needs_input_grad[0]:
             acc = None
-            wide = {} if weight.dtype == torch.float32 else {"out_dtype": torch.float32}
             for n0, n1 in blocks:
-                part = torch.mm(gy2[:, n0:n1], weight[n0:n1], **wide)
+                part = torch.mm(gy2[:, n0:n1], wd[n0:n1], **wide)
                 acc = part if acc is None else acc.add_(part)
-            dx = acc.to(x2.dtype).view(ctx.x_shape)
+            dx = acc.to(x_dtype).view(ctx.x_shape)
         if ctx.needs_input_grad[1]:
-            dw = torch.empty_like(weight)
+            # fp32 straight from the GEMMs for an fp32 weight; otherwise in the
+            # operand dtype.
+            fp32_out = w_dtype == torch.float32
+            dw = torch.empty(n, k, device=wd.device, dtype=torch.float32 if fp32_out else wd.dtype)
             for n0, n1 in blocks:
-                torch.mm(gy2[:, n0:n1].t(), x2, out=dw[n0:n1])
-        return dx, dw
+                torch.mm(gy2[:, n0:n1].t(), x2, **(wide if fp32_out else {}), out=dw[n0:n1])
+            dw = dw.to(w_dtype)
+        return dx, dw, None
 
 
 def wide_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
@@ -90,23 +105,25 @@ def wide_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     backward blocked the same way).
 
     Used on a GPU when the weight exceeds the bound and x has at least
-    WIDE_LINEAR_MIN_ROWS rows; everything else takes F.linear. Under autocast the operands are cast to the autocast
-    dtype first, as F.linear's autocast rule does. Each output element is the
-    same K-reduction as in one launch.
+    WIDE_LINEAR_MIN_ROWS rows; everything else takes F.linear. Under autocast
+    the operands are cast to the autocast dtype, as F.linear's autocast rule
+    does. Each output element is the same K-reduction as in one launch.
     """
     n, k = weight.shape
     rows = x.numel() // k if k else 0
     if (n * k * weight.element_size() <= WIDE_LINEAR_CHUNK_BYTES or rows < WIDE_LINEAR_MIN_ROWS
             or not x.is_cuda or not weight.is_cuda):
         return F.linear(x, weight)
+    dtype = None
     if torch.is_autocast_enabled(x.device.type):
-        dt = torch.get_autocast_dtype(x.device.type)
-        x, weight = x.to(dt), weight.to(dt)
-    if x.dtype != weight.dtype:
+        dtype = torch.get_autocast_dtype(x.device.type)
+    elif x.dtype != weight.dtype:
         return F.linear(x, weight)  # raises torch's dtype error
     with torch.autocast(x.device.type, enabled=False):
         if torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad):
-            return _WideLinearFunction.apply(x, weight)
+            return _WideLinearFunction.apply(x, weight, dtype)
+        if dtype is not None:
+            x, weight = x.to(dtype), weight.to(dtype)
         x2 = x.reshape(-1, k)
         out = torch.empty(*x.shape[:-1], n, device=x.device, dtype=x.dtype)
         _wide_forward(x2, weight, out.view(-1, n))
