@@ -56,11 +56,24 @@ constexpr int MODE_DL = 0;
 constexpr int MODE_Q = 1;
 constexpr int kSsmThreads = 256;
 
-// Raw bits of N consecutive storage elements (unpacked only on use).
+// Raw bits of N consecutive storage elements (unpacked only on use). A single
+// 16-bit element is kept in a 16-bit field: held in 32 bits, the zero-extension
+// of a 16-bit buffer load is materialised (v_and) right after the load is
+// issued, with a wait for that load in front of it, which stalls the wave on
+// every prefetch; in 16 bits it folds into the unpack at the point of use.
+template <int BYTES>
+struct RawBits {
+  uint32_t w[(BYTES + 3) / 4];
+  __device__ uint32_t word(int i) const { return w[i]; }
+};
+template <>
+struct RawBits<2> {
+  uint16_t h;
+  __device__ uint32_t word(int) const { return h; }
+};
 template <typename T, int N>
-struct Raw {
+struct Raw : RawBits<N * (int)sizeof(T)> {
   static constexpr int W = (N * (int)sizeof(T) + 3) / 4;
-  uint32_t w[W];
 };
 
 // Load N elements from a byte address (base + 32-bit lane offset).
@@ -85,19 +98,64 @@ __device__ inline void raw_load(const char* __restrict__ p, Raw<T, N>& r) {
     r.w[0] = *reinterpret_cast<const uint32_t*>(p);
   } else {
     static_assert(bytes == 2, "unsupported raw width");
-    r.w[0] = *reinterpret_cast<const uint16_t*>(p);
+    r.h = *reinterpret_cast<const uint16_t*>(p);
+  }
+}
+
+// Buffer resource over memory from p on: raw (unswizzled), stride 0, the
+// maximum record count, gfx9's 32-bit data-format word. Loads through it take
+// a scalar base (rebuilt per step from SGPRs) plus a 32-bit per-lane offset in
+// one VGPR, so the per-step addressing costs no VALU instructions; with global
+// loads the compiler keeps a 64-bit lane pointer per tensor and adds the step
+// offset to it on the VALU every step.
+__device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
+}
+
+// Load N elements at byte offset voff of a buffer.
+template <typename T, int N>
+__device__ inline void raw_load_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, Raw<T, N>& r) {
+  constexpr int bytes = N * (int)sizeof(T);
+  if constexpr (bytes % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < bytes / 16; ++i) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 * i, 0, 0);
+      r.w[4 * i + 0] = v[0];
+      r.w[4 * i + 1] = v[1];
+      r.w[4 * i + 2] = v[2];
+      r.w[4 * i + 3] = v[3];
+    }
+  } else if constexpr (bytes == 8) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, 0, 0);
+    r.w[0] = v[0];
+    r.w[1] = v[1];
+  } else if constexpr (bytes == 4) {
+    r.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, 0, 0);
+  } else {
+    static_assert(bytes == 2, "unsupported raw width");
+    r.h = __builtin_amdgcn_raw_buffer_load_b16(rs, voff, 0, 0);
+  }
+}
+
+// Store one element (converted from fp32) at byte offset voff of a buffer.
+template <typename T>
+__device__ inline void store_elem_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, float v) {
+  if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rs, voff, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(io<T>::from_f32(v).bits, rs, voff, 0, 0);
   }
 }
 
 template <typename T, int N>
 __device__ inline float raw_get(const Raw<T, N>& r, int e) {
   if constexpr (sizeof(T) == 4) {
-    return __uint_as_float(r.w[e]);
+    return __uint_as_float(r.word(e));
   } else if constexpr (std::is_same<T, bf16_t>::value) {
-    const uint32_t word = r.w[e >> 1];
+    const uint32_t word = r.word(e >> 1);
     return __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
   } else {
-    const uint32_t word = r.w[e >> 1];
+    const uint32_t word = r.word(e >> 1);
     return io<T>::bits_to_f32((e & 1) ? (word >> 16) : (word & 0xffffu));
   }
 }
@@ -256,14 +314,17 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   const bool kvalid = FULL || k0 < a.S;
   if (!kvalid) k0 = (int)a.S - KPL;
 
-  const int64_t Tn = a.T;
+  // Step counters are 32-bit (the host checks T): gfx9's scalar unit has no
+  // 64-bit compares, and 64-bit ones would run on the VALU every step.
+  const int Tn = (int)a.T;
   const int64_t rowBC = a.Dm * a.S * 4;  // elements per (b, t) slice of B, C, q
   const int64_t rowTok = a.Dm;           // elements per (b, t) slice of delta, s
   // Byte offsets of this lane inside one (b, t) slice (the host checks that a
-  // slice is below 2 GiB).
+  // slice, and the strided D vector, stay below 2 GiB).
   const uint32_t offBC = (uint32_t)((d * a.S + k0) * 4 * (int64_t)sizeof(T));
   const uint32_t offTok = (uint32_t)(d * (int64_t)sizeof(T));
   const uint32_t offQ4 = (uint32_t)(d * 4 * (int64_t)sizeof(T));
+  const uint32_t offD = (uint32_t)(d * a.d_sd * (int64_t)sizeof(T));
 
   // Per-(d,k) constants of the Cayley closed form (MODE_DL).
   LamConst lam[KPL];
@@ -285,38 +346,41 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
     for (int kk = 0; kk < KPL; ++kk) h[kk] = quat_from(&e[4 * kk]);
   }
 
-  // Loads of step t into a ring slot; t is wave-uniform, so every slice base
-  // below is a scalar and the lane adds only its 32-bit offset.
-  auto load_step = [&](Step<T, MODE, KPL>& st, int64_t t) {
+  // Loads of step t into a ring slot. t is wave-uniform: each tensor's slice
+  // base goes into a buffer descriptor (SGPRs) and the lane supplies only its
+  // 32-bit byte offset inside the slice.
+  auto load_step = [&](Step<T, MODE, KPL>& st, int t) {
     const int64_t rt = b * Tn + t;
     if constexpr (MODE == MODE_DL) {
-      raw_load<T, 1>((const char*)((const T*)a.delta + rt * rowTok) + offTok, st.delta);
-      raw_load<T, 1>((const char*)((const T*)a.s + rt * rowTok) + offTok, st.s);
+      raw_load_buf<T, 1>(buf_rsrc((const T*)a.delta + rt * rowTok), offTok, st.delta);
+      raw_load_buf<T, 1>(buf_rsrc((const T*)a.s + rt * rowTok), offTok, st.s);
     } else {
-      raw_load<T, 4>((const char*)((const T*)a.Sq + rt * rowTok * 4) + offQ4, st.S);
-      raw_load<T, 1>((const char*)((const T*)a.Dq + b * a.d_sb + t * a.d_st + d * a.d_sd), st.D);
-      raw_load<T, 4 * KPL>((const char*)((const T*)a.q + rt * rowBC) + offBC, st.q);
+      raw_load_buf<T, 4>(buf_rsrc((const T*)a.Sq + rt * rowTok * 4), offQ4, st.S);
+      raw_load_buf<T, 1>(buf_rsrc((const T*)a.Dq + b * a.d_sb + (int64_t)t * a.d_st), offD, st.D);
+      raw_load_buf<T, 4 * KPL>(buf_rsrc((const T*)a.q + rt * rowBC), offBC, st.q);
     }
-    raw_load<T, 4 * KPL>((const char*)((const T*)a.Bm + rt * rowBC) + offBC, st.B);
-    raw_load<T, 4 * KPL>((const char*)((const T*)a.Cm + rt * rowBC) + offBC, st.C);
+    raw_load_buf<T, 4 * KPL>(buf_rsrc((const T*)a.Bm + rt * rowBC), offBC, st.B);
+    raw_load_buf<T, 4 * KPL>(buf_rsrc((const T*)a.Cm + rt * rowBC), offBC, st.C);
   };
 
   Step<T, MODE, KPL> ring[PF];
-  const int64_t t_last = Tn - 1;
+  const int t_last = Tn - 1;
 #pragma unroll
   for (int i = 0; i < PF; ++i) load_step(ring[i], i < Tn ? i : t_last);
 
   const bool writer = gvalid && (G < 4 || j < 4);
   const int64_t rowY = a.Dm * 4;
+  const uint32_t offY = (uint32_t)(d * 4 * (int64_t)sizeof(T));
   // Checkpoint schedule (scalar): the next step whose state is saved.
-  const int64_t n_ckpt = a.h_ckpt ? (Tn + a.ckpt_every - 1) / a.ckpt_every : 0;
-  int64_t next_ckpt = a.h_ckpt ? (a.ckpt_every < Tn ? a.ckpt_every - 1 : Tn - 1) : -1;
+  const int ckpt_every = (int)a.ckpt_every;
+  const int64_t n_ckpt = a.h_ckpt ? (Tn + ckpt_every - 1) / ckpt_every : 0;
+  int next_ckpt = a.h_ckpt ? (ckpt_every < Tn ? ckpt_every - 1 : Tn - 1) : -1;
   int64_t ckpt_idx = 0;
 
-  for (int64_t t0 = 0; t0 < Tn; t0 += PF) {
+  for (int t0 = 0; t0 < Tn; t0 += PF) {
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      const int64_t t = t0 + i;
+      const int t = t0 + i;
       if (t >= Tn) break;
       Step<T, MODE, KPL>& cur = ring[i];
 
@@ -350,7 +414,7 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
       // Refill the consumed slot with step t + PF (clamped: the tail re-reads
       // the last step, which keeps the loads unconditional).
       {
-        const int64_t tn = t + PF;
+        const int tn = t + PF;
         load_step(cur, tn < Tn ? tn : t_last);
       }
       if constexpr (!FULL) {
@@ -361,7 +425,7 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
       int c0;
       const int nc = group_reduce<G>(acc, lane, v, c0);
       if (writer) {
-        T* yo = (T*)a.y + (b * Tn + t) * rowY + d * 4;
+        const __amdgpu_buffer_rsrc_t ry = buf_rsrc((T*)a.y + (b * Tn + t) * rowY);
         if constexpr (MODE == MODE_DL) {
           if (c0 == 0) v[0] = fmaf(dskip, sv, v[0]);
         } else {
@@ -371,7 +435,7 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (e < nc) store_scalar(yo + c0 + e, v[e]);
+          if (e < nc) store_elem_buf<T>(ry, offY + (uint32_t)((c0 + e) * (int)sizeof(T)), v[e]);
       }
       if (a.h_ckpt && t == next_ckpt) {
         // Chunk t / ckpt_every ends here (or the sequence does).
@@ -385,7 +449,7 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
           store_vec<float, 4 * KPL>(a.h_ckpt + (((b * n_ckpt + ckpt_idx) * a.Dm + d) * a.S + k0) * 4, e);
         }
         ++ckpt_idx;
-        next_ckpt = next_ckpt + a.ckpt_every < Tn ? next_ckpt + a.ckpt_every : Tn - 1;
+        next_ckpt = next_ckpt + ckpt_every < Tn ? next_ckpt + ckpt_every : Tn - 1;
       }
       if constexpr (SYNC == 1) __syncthreads();
     }
@@ -461,8 +525,13 @@ int launch_ssm_kpl(const SsmArgs& a, hipStream_t s) {
 template <typename T, int MODE>
 int launch_ssm(const SsmArgs& a, hipStream_t s) {
   if (a.batch == 0 || a.T == 0 || a.Dm == 0) return MQC_OK;
-  // Per-(b, t) slices are addressed with 32-bit lane offsets.
+  // Per-(b, t) slices (and the strided D vector) are addressed with 32-bit lane
+  // offsets; step counters are 32-bit.
   if (a.Dm * a.S * 4 * (int64_t)sizeof(T) >= ((int64_t)1 << 31)) return MQC_E_LIMIT;
+  if (a.T >= ((int64_t)1 << 30) || (a.h_ckpt && (a.ckpt_every < 1 || a.ckpt_every >= (1 << 30))))
+    return MQC_E_LIMIT;
+  if (MODE == MODE_Q && (a.d_sd < 0 || (a.Dm - 1) * a.d_sd * (int64_t)sizeof(T) >= ((int64_t)1 << 31)))
+    return MQC_E_LIMIT;
   const uintptr_t qa = 4 * sizeof(T);
   if (!aligned(a.Bm, qa) || !aligned(a.Cm, qa) || !aligned(a.y, sizeof(T)) ||
       (MODE == MODE_Q && (!aligned(a.q, qa) || !aligned(a.Sq, qa) || !aligned(a.Dq, sizeof(T)))) ||
