@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/mambaqc_hip.h"
 
 namespace mqc {
@@ -107,6 +109,22 @@ __device__ inline void load_vec<bf16_t, 8>(const bf16_t* __restrict__ p, float (
   }
 }
 
+// Two fp32 values rounded to the 16-bit storage type and packed (lo in bits
+// 0-15): one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950, round to nearest
+// even like the scalar conversions above.
+template <typename T>
+__device__ inline uint32_t pack2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    typedef __bf16 h16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, h16x2));
+  } else {
+    static_assert(std::is_same<T, f16_t>::value, "pack2 takes a 16-bit storage type");
+    typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, h16x2));
+  }
+}
+
 template <typename T, int N>
 __device__ inline void store_vec(T* __restrict__ p, const float (&in)[N]) {
   if constexpr (sizeof(T) == 4) {
@@ -124,8 +142,8 @@ __device__ inline void store_vec(T* __restrict__ p, const float (&in)[N]) {
     static_assert(N % 4 == 0, "16-bit stores come in 4-element units");
 #pragma unroll
     for (int i = 0; i < N / 4; ++i) {
-      uint32_t lo = io<T>::from_f32(in[4 * i + 0]).bits | ((uint32_t)io<T>::from_f32(in[4 * i + 1]).bits << 16);
-      uint32_t hi = io<T>::from_f32(in[4 * i + 2]).bits | ((uint32_t)io<T>::from_f32(in[4 * i + 3]).bits << 16);
+      const uint32_t lo = pack2<T>(in[4 * i + 0], in[4 * i + 1]);
+      const uint32_t hi = pack2<T>(in[4 * i + 2], in[4 * i + 3]);
       reinterpret_cast<uint2*>(p)[i] = make_uint2(lo, hi);
     }
   }

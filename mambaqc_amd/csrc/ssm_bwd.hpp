@@ -29,6 +29,22 @@
 
 namespace mqc {
 
+// Store one quaternion (converted from fp32) at byte offset voff + soff of a buffer.
+template <typename T>
+__device__ inline void store_quat_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, const float (&e)[4],
+                                      uint32_t soff) {
+  if constexpr (sizeof(T) == 4) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = {__float_as_uint(e[0]), __float_as_uint(e[1]), __float_as_uint(e[2]),
+                     __float_as_uint(e[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, voff, soff, 0);
+  } else {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = {pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3])};
+    __builtin_amdgcn_raw_buffer_store_b64(v, rs, voff, soff, 0);
+  }
+}
+
 struct SsmBwdArgs {
   const void* delta;  // [B,T,D] dtype
   const void* s;      // [B,T,D] dtype
@@ -133,8 +149,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
   const int64_t k = kvalid ? j : a.S - 1;
   const bool own = gvalid && kvalid;
 
-  const int64_t Tn = a.T;
-  const int64_t nC = (Tn + K - 1) / K;
+  // 32-bit step and chunk counters (the host checks T): gfx9's scalar unit has
+  // no 64-bit compares.
+  const int Tn = (int)a.T;
+  const int nC = (Tn + K - 1) / K;
   const int64_t rowBC = a.Dm * a.S * 4;
   const int64_t rowTok = a.Dm;
   const int64_t rowY = a.Dm * 4;
@@ -156,9 +174,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
   }
 
   // Operands of one chunk: the K steps' delta, s, B, C, gy (raw bits) and the
-  // checkpointed state before the chunk. Addresses are a chunk base (uniform)
-  // plus a 32-bit per-lane offset; the launcher checks that K steps of every
-  // tensor fit in 32 bits.
+  // checkpointed state before the chunk. Every tensor is read and written
+  // through a buffer descriptor on the chunk's first row (SGPRs, rebuilt per
+  // chunk); step i adds the scalar i * step bytes and the lane its fixed 32-bit
+  // offset, so no addressing runs on the VALU. The launcher checks that K steps
+  // of every tensor fit in 32 bits.
   struct Ops {
     Raw<T, 1> rd[K], rs[K];
     Raw<T, 4> rB[K], rC[K], rg[K];
@@ -169,35 +189,35 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
   const uint32_t stepY = (uint32_t)(rowY * (int64_t)sizeof(T));
   const uint32_t stepF = (uint32_t)(rowTok * 4);  // fp32 d_delta, d_s
   const uint32_t offF = (uint32_t)(d * 4);
-  auto load_chunk = [&](Ops& o, int64_t c, int len) {
-    const int64_t row0 = b * Tn + c * K;
-    const char* pD = (const char*)a.delta + row0 * stepTok;
-    const char* pS = (const char*)a.s + row0 * stepTok;
-    const char* pB = (const char*)a.Bm + row0 * (int64_t)stepBC;
-    const char* pC = (const char*)a.Cm + row0 * (int64_t)stepBC;
-    const char* pG = (const char*)a.gy + row0 * (int64_t)stepY;
+  auto load_chunk = [&](Ops& o, int c, int len) {
+    const int64_t row0 = b * Tn + (int64_t)c * K;
+    const __amdgpu_buffer_rsrc_t rD = buf_rsrc((const char*)a.delta + row0 * stepTok);
+    const __amdgpu_buffer_rsrc_t rS = buf_rsrc((const char*)a.s + row0 * stepTok);
+    const __amdgpu_buffer_rsrc_t rB = buf_rsrc((const char*)a.Bm + row0 * (int64_t)stepBC);
+    const __amdgpu_buffer_rsrc_t rC = buf_rsrc((const char*)a.Cm + row0 * (int64_t)stepBC);
+    const __amdgpu_buffer_rsrc_t rG = buf_rsrc((const char*)a.gy + row0 * (int64_t)stepY);
 #pragma unroll
     for (int i = 0; i < K; ++i) {
       // A tail chunk re-reads its last step.
       const uint32_t ii = (uint32_t)(i < len ? i : len - 1);
-      raw_load<T, 1>(pD + ii * (int64_t)stepTok + offTok, o.rd[i]);
-      raw_load<T, 1>(pS + ii * (int64_t)stepTok + offTok, o.rs[i]);
-      raw_load<T, 4>(pB + ii * (int64_t)stepBC + offBC, o.rB[i]);
-      raw_load<T, 4>(pC + ii * (int64_t)stepBC + offBC, o.rC[i]);
-      raw_load<T, 4>(pG + ii * (int64_t)stepY + offY, o.rg[i]);
+      raw_load_buf<T, 1>(rD, offTok, o.rd[i], ii * stepTok);
+      raw_load_buf<T, 1>(rS, offTok, o.rs[i], ii * stepTok);
+      raw_load_buf<T, 4>(rB, offBC, o.rB[i], ii * stepBC);
+      raw_load_buf<T, 4>(rC, offBC, o.rC[i], ii * stepBC);
+      raw_load_buf<T, 4>(rG, offY, o.rg[i], ii * stepY);
     }
     // The checkpoint of the previous chunk (chunk 0 starts from h0, read in process).
     const int64_t cp = c > 0 ? c - 1 : 0;
     o.h_in = *reinterpret_cast<const float4*>(a.h_ckpt + (((b * nC + cp) * a.Dm + d) * a.S + k) * 4);
   };
   // FULLC: all K steps of the chunk exist (every chunk but a ragged last one).
-  auto process_chunk = [&](auto fullc, Ops& o, int64_t c, int len) {
+  auto process_chunk = [&](auto fullc, Ops& o, int c, int len) {
     constexpr bool FULLC = decltype(fullc)::value;
-    const int64_t row0 = b * Tn + c * K;
-    char* pdB = (char*)a.dB + row0 * (int64_t)stepBC;
-    char* pdC = (char*)a.dC + row0 * (int64_t)stepBC;
-    char* pdd = (char*)a.d_delta + row0 * (int64_t)stepF;
-    char* pds = (char*)a.d_s + row0 * (int64_t)stepF;
+    const int64_t row0 = b * Tn + (int64_t)c * K;
+    const __amdgpu_buffer_rsrc_t rdB = buf_rsrc((char*)a.dB + row0 * (int64_t)stepBC);
+    const __amdgpu_buffer_rsrc_t rdC = buf_rsrc((char*)a.dC + row0 * (int64_t)stepBC);
+    const __amdgpu_buffer_rsrc_t rdd = buf_rsrc((char*)a.d_delta + row0 * (int64_t)stepF);
+    const __amdgpu_buffer_rsrc_t rds = buf_rsrc((char*)a.d_s + row0 * (int64_t)stepF);
     quat hs[K + 1];
     float rq[K];  // 1 / max(N, eps) of each step, negated where the clamp engaged
     if (c > 0) {
@@ -249,19 +269,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
         if (own) {
           const float eB[4] = {sv * g.w, sv * g.x, sv * g.y, sv * g.z};
           const float eC[4] = {dC.w, dC.x, dC.y, dC.z};
-          store_vec<T, 4>((T*)(pdB + i * (int64_t)stepBC + offBC), eB);
-          store_vec<T, 4>((T*)(pdC + i * (int64_t)stepBC + offBC), eC);
+          store_quat_buf<T>(rdB, offBC, eB, (uint32_t)i * stepBC);
+          store_quat_buf<T>(rdC, offBC, eC, (uint32_t)i * stepBC);
         } else {
           ddl = 0.f;
           dsk = 0.f;
         }
         group_reduce2<G>(ddl, dsk, lane);
-        if (gvalid) {
-          if (j == 0) *(float*)(pdd + i * (int64_t)stepF + offF) = ddl;
-          if (j == (G > 1 ? 1 : 0)) {
-            *(float*)(pds + i * (int64_t)stepF + offF) = fmaf(Dv, gy.w, dsk);
-            dD = fmaf(gy.w, sv, dD);
-          }
+        // Lane 0 holds the d delta total and lane 1 the ds total; one DPP read
+        // brings the latter to lane 0, which stores both. (Stores from two
+        // lanes under different conditions get merged by the compiler into
+        // one store whose buffer descriptor is lane-dependent, which costs a
+        // waterfall loop.)
+        const float ds_tot = G > 1 ? lane_xor1(dsk) : dsk;
+        if (gvalid && j == 0) {
+          store_elem_buf<float>(rdd, offF, ddl, (uint32_t)i * stepF);
+          store_elem_buf<float>(rds, offF, fmaf(Dv, gy.w, ds_tot), (uint32_t)i * stepF);
+          dD = fmaf(gy.w, sv, dD);
         }
       }
     }
@@ -270,7 +294,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
 
   Ops buf;
   {
-    const int64_t c = nC - 1;
+    const int c = nC - 1;
     const int len = (int)(Tn - c * K);
     load_chunk(buf, c, len);
     if (len == K)
@@ -278,7 +302,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
     else
       process_chunk(std::integral_constant<bool, false>{}, buf, c, len);
   }
-  for (int64_t c = nC - 2; c >= 0; --c) {
+  for (int c = nC - 2; c >= 0; --c) {
     load_chunk(buf, c, K);
     process_chunk(std::integral_constant<bool, true>{}, buf, c, K);
   }
@@ -297,7 +321,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
     di[1] = dv[1] * (1.f - L.v1 * L.v1);
     di[2] = dv[2] * (1.f - L.v2 * L.v2);
   }
-  if (gvalid && j == (G > 1 ? 1 : 0)) a.dD_part[b * a.Dm + d] = dD;
+  if (gvalid && j == 0) a.dD_part[b * a.Dm + d] = dD;
 }
 
 // Checkpoint interval the backward needs: the chunk's operands and states live
@@ -326,6 +350,7 @@ int launch_ssm_bwd(const SsmBwdArgs& a, hipStream_t s) {
   // K consecutive steps of one tensor must be addressable with 32-bit offsets.
   if (a.Dm * a.S * 4 * (int64_t)sizeof(T) * ssm_bwd_chunk<T>() >= ((int64_t)1 << 32))
     return MQC_E_LIMIT;
+  if (a.T >= ((int64_t)1 << 30)) return MQC_E_LIMIT;
   const uintptr_t qa = 4 * sizeof(T);
   if (!aligned(a.Bm, qa) || !aligned(a.Cm, qa) || !aligned(a.gy, qa) || !aligned(a.dB, qa) ||
       !aligned(a.dC, qa) || !aligned(a.h_ckpt, 16) || (a.h0 && !aligned(a.h0, qa)) ||

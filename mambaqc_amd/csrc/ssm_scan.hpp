@@ -112,38 +112,41 @@ __device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void* p) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
 }
 
-// Load N elements at byte offset voff of a buffer.
+// Load N elements at byte offset voff (per lane) + soff (wave-uniform, added
+// by the buffer unit from an SGPR) of a buffer.
 template <typename T, int N>
-__device__ inline void raw_load_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, Raw<T, N>& r) {
+__device__ inline void raw_load_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, Raw<T, N>& r,
+                                    uint32_t soff = 0) {
   constexpr int bytes = N * (int)sizeof(T);
   if constexpr (bytes % 16 == 0) {
 #pragma unroll
     for (int i = 0; i < bytes / 16; ++i) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 * i, 0, 0);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 * i, soff, 0);
       r.w[4 * i + 0] = v[0];
       r.w[4 * i + 1] = v[1];
       r.w[4 * i + 2] = v[2];
       r.w[4 * i + 3] = v[3];
     }
   } else if constexpr (bytes == 8) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0);
     r.w[0] = v[0];
     r.w[1] = v[1];
   } else if constexpr (bytes == 4) {
-    r.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, 0, 0);
+    r.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, 0);
   } else {
     static_assert(bytes == 2, "unsupported raw width");
-    r.h = __builtin_amdgcn_raw_buffer_load_b16(rs, voff, 0, 0);
+    r.h = __builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff, 0);
   }
 }
 
-// Store one element (converted from fp32) at byte offset voff of a buffer.
+// Store one element (converted from fp32) at byte offset voff + soff of a buffer.
 template <typename T>
-__device__ inline void store_elem_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, float v) {
+__device__ inline void store_elem_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, float v,
+                                      uint32_t soff = 0) {
   if constexpr (sizeof(T) == 4) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rs, voff, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rs, voff, soff, 0);
   } else {
-    __builtin_amdgcn_raw_buffer_store_b16(io<T>::from_f32(v).bits, rs, voff, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(io<T>::from_f32(v).bits, rs, voff, soff, 0);
   }
 }
 
