@@ -138,6 +138,25 @@ def test_training_validation_codes_without_gpu():
     assert lib.mqc_out_gate_bwd(FAKE, FAKE, 8, FAKE, FAKE, FAKE, 2, 8, 4, 0, None) == -2
 
 
+def test_step_counter_limits_without_gpu():
+    """The SSM kernels count steps in 32 bits and address D through a 32-bit
+    lane offset: the entry points refuse T >= 2^30 and a negative D stride
+    before any HIP call."""
+    lib = nat.load()
+    T = 1 << 30
+    P = [FAKE] * 7
+    assert lib.mqc_ssm_fused_fwd(*P, None, FAKE, None, 1, T, 2, 8, 1e-6, 1, None) == -5
+    assert lib.mqc_ssm_q_fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 0, 1, None, FAKE, None,
+                             1, T, 2, 8, 0, None) == -5
+    assert lib.mqc_ssm_q_fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 0, -1, None, FAKE, None,
+                             1, 4, 2, 8, 0, None) == -5
+    assert lib.mqc_ssm_fused_fwd_train(*P, None, FAKE, None, FAKE, 8, 1, T, 2, 8,
+                                       1e-6, 1, None) == -5
+    G = [FAKE] * 7
+    assert lib.mqc_ssm_fused_bwd(*P, None, FAKE, 8, FAKE, None, *G, None, 1, T, 2, 8,
+                                 1e-6, 1, None) == -5
+
+
 def test_block_seeded_init_matches_reference():
     info = json.loads((GOLDEN / "init_c1.json").read_text())
     torch.manual_seed(0)
