@@ -36,7 +36,10 @@ extern "C" {
 #define MQC_E_SHAPE (-2)     /* a size is negative or inconsistent */
 #define MQC_E_DTYPE (-3)     /* unknown dtype code */
 #define MQC_E_ALIGN (-4)     /* a pointer is not aligned for the vector loads */
-#define MQC_E_LIMIT (-5)     /* a size is beyond what the kernels support */
+#define MQC_E_LIMIT (-5)     /* a size is beyond what the kernels support (for the
+                              * SSM entry points: seq_len >= 2^30, d_state above the
+                              * stated maximum, one (b, t) slice of B/C of 2 GiB or
+                              * more, or a negative or too large D stride) */
 
 /* Human-readable text for a status code (static storage, never NULL). */
 const char* mqc_status_string(int status);
