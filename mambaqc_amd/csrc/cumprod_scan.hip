@@ -73,7 +73,7 @@ __global__ __launch_bounds__(W * 64) void cumprod_scan_kernel(const T* __restric
         if (j < n) {
           quat r = qmul(v[j], E);
           float e[4] = {r.w, r.x, r.y, r.z};
-          store_vec<T, 4>(ob + (t0 + j) * row, e);
+          store_vec<T, 4, true>(ob + (t0 + j) * row, e);
         }
       }
     }

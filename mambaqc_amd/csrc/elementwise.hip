@@ -47,7 +47,7 @@ __global__ __launch_bounds__(kThreads) void map_kernel(const T* __restrict__ a,
       float vo[E];
 #pragma unroll
       for (int qd = 0; qd < QV; ++qd) op(&va[u][4 * qd], b ? &vb[u][4 * qd] : nullptr, &vo[4 * qd]);
-      store_vec<T, E>(out + (i + u * stride) * E, vo);
+      store_vec<T, E, true>(out + (i + u * stride) * E, vo);
     }
   }
   for (; i < n_vec; i += stride) {
@@ -56,7 +56,7 @@ __global__ __launch_bounds__(kThreads) void map_kernel(const T* __restrict__ a,
     if (b) load_vec<T, E>(b + i * E, vb);
 #pragma unroll
     for (int qd = 0; qd < QV; ++qd) op(&va[4 * qd], b ? &vb[4 * qd] : nullptr, &vo[4 * qd]);
-    store_vec<T, E>(out + i * E, vo);
+    store_vec<T, E, true>(out + i * E, vo);
   }
   // Tail quaternions that do not fill a vector (only when QV > 1).
   if (QV > 1 && blockIdx.x == 0) {
