@@ -233,6 +233,26 @@ __device__ inline float sum_halves_to_low(float v) {
 }
 
 // ---------------------------------------------------------------------------
+// XCD-aware block order. MI355X dispatches the workgroups of a launch to its 8
+// XCDs (each with its own L2) round-robin by linear block id, so neighbouring
+// blocks land on different L2s. Where neighbouring blocks share cache lines
+// (the SSM kernels: a few d's per block, so one line of delta, s, gy, y or of
+// the fp32 d_delta / d_s spans several blocks), every XCD fetches the line or
+// writes part of it. This remap gives each XCD a contiguous range of logical
+// blocks; it is the identity when the block count is not a multiple of 8.
+// ---------------------------------------------------------------------------
+constexpr int kXCDs = 8;
+
+__device__ inline void xcd_block(int64_t& bx, int64_t& by) {
+  const int64_t gx = gridDim.x;
+  const int64_t n = gx * gridDim.y;
+  const int64_t lin = blockIdx.x + (int64_t)blockIdx.y * gx;
+  const int64_t logical = n % kXCDs ? lin : (lin % kXCDs) * (n / kXCDs) + lin / kXCDs;
+  bx = logical % gx;
+  by = logical / gx;
+}
+
+// ---------------------------------------------------------------------------
 // Launch helpers
 // ---------------------------------------------------------------------------
 inline int launch_status() {
