@@ -220,7 +220,11 @@ def _dl_inputs(b, T, d, k, seed, dtype):
 
 
 @pytest.mark.parametrize("shape", [(1, 64, 8, 64), (2, 33, 5, 16), (1, 17, 3, 1), (2, 10, 4, 3),
-                                   (1, 12, 2, 100), (1, 9, 130, 2)])
+                                   (1, 12, 2, 100), (1, 9, 130, 2),
+                                   # block counts that are (2 x 8 = 16, 4 x 12 = 48) and are not
+                                   # (3 x 13 = 39) multiples of the 8 XCDs: the remapped and the
+                                   # hardware block order
+                                   (2, 37, 64, 64), (4, 19, 96, 64), (3, 21, 100, 64)])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_ssm_fused_dl(shape, dtype):
     a = _dl_inputs(*shape, seed=sum(shape), dtype=dtype)
