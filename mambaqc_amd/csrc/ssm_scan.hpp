@@ -550,6 +550,12 @@ int launch_ssm(const SsmArgs& a, hipStream_t s) {
            (!a.h_last || aligned(a.h_last, al));
   };
   if constexpr (sizeof(T) == 2) {
+    // Two states per lane fill the machine at config 3 (3072 waves, 12 per CU:
+    // 2.34 ms against 2.74 with one state per lane). With fewer waves than that
+    // (small batch x d_inner), one state per lane doubles the lanes: measured at
+    // T 2048, D 1536, S 64: batch 1 1.063 -> 1.001 ms, batch 2 1.391 -> 1.340 ms.
+    const int64_t waves_kpl2 = a.batch * a.Dm * ((a.S + 1) / 2) / 64;
+    if (a.S <= 64 && waves_kpl2 < 12 * kCUs) return launch_ssm_kpl<T, MODE, 1>(a, s);
     if (a.S <= 128 && wide_ok(2)) return launch_ssm_kpl<T, MODE, 2>(a, s);
     if (a.S <= 64) return launch_ssm_kpl<T, MODE, 1>(a, s);
     if (a.S <= 256 && wide_ok(4)) return launch_ssm_kpl<T, MODE, 4>(a, s);

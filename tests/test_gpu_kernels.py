@@ -224,7 +224,10 @@ def _dl_inputs(b, T, d, k, seed, dtype):
                                    # block counts that are (2 x 8 = 16, 4 x 12 = 48) and are not
                                    # (3 x 13 = 39) multiples of the 8 XCDs: the remapped and the
                                    # hardware block order
-                                   (2, 37, 64, 64), (4, 19, 96, 64), (3, 21, 100, 64)])
+                                   (2, 37, 64, 64), (4, 19, 96, 64), (3, 21, 100, 64),
+                                   # enough (b, d) for two states per lane in 16-bit storage
+                                   # (>= 12 waves per CU) and 768-thread blocks; d ragged
+                                   (8, 5, 768, 64), (3, 7, 2050, 64)])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_ssm_fused_dl(shape, dtype):
     a = _dl_inputs(*shape, seed=sum(shape), dtype=dtype)
