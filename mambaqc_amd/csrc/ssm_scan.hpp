@@ -495,20 +495,44 @@ int launch_ssm_g(const SsmArgs& a, hipStream_t s) {
 // step), so at any moment a block reads one contiguous span of each (b, t)
 // slice of B and C instead of scattered 1 KiB pieces at drifting t: DRAM row
 // locality, measured on MI355X at 4.76 -> 5.44 TB/s for the config-3 shape.
-// 768-thread blocks (12 waves: one block per CU at <= 168 VGPRs, 24 KiB of
-// each slice per step with G = 32) are used when there are enough of them to
-// give every CU one; smaller problems use 256-thread blocks.
+// Every block walks all T steps, so the busiest CU sets the time: the shape is
+// the one that minimises ceil(blocks / CUs) * waves per block, the waves of
+// work that CU carries; ties go to 768, 1024, 512, 256 threads in that order
+// (768 measured best where it fills the machine exactly). Measured at B4 T2048
+// S64 (bf16): d_inner 1536: 768 threads 2.33 ms, 1024 2.55, 512 2.62;
+// d_inner 2048: 768 threads (344 blocks, a second round for 88 CUs) 3.81 ms,
+// 1024 (256 blocks) 3.04, 512 3.18; d_inner 1024 (one state per lane):
+// 768 threads 2.53 ms, 1024 1.70.
 constexpr int kCUs = 256;  // MI355X compute units
+
+inline int64_t busiest_cu_waves(const SsmArgs& a, int G, int NT) {
+  const int64_t gpb = NT / G;
+  const int64_t blocks = a.batch * ((a.Dm + gpb - 1) / gpb);
+  return (blocks + kCUs - 1) / kCUs * (NT / 64);
+}
 
 template <typename T, int MODE, int KPL, int G>
 int launch_ssm_shape(const SsmArgs& a, hipStream_t s) {
   constexpr int PF = ssm_prefetch<T, KPL>();
-  if constexpr (G >= 8) {
-    constexpr int GPB = 768 / G;
-    if (a.batch * ((a.Dm + GPB - 1) / GPB) >= kCUs)
-      return launch_ssm_g<T, MODE, KPL, G, PF, 768, 1>(a, s);
+  int best = 256;
+  if constexpr (G <= 64) {
+    const int order[4] = {768, 1024, 512, 256};
+    int64_t best_w = -1;
+    for (int nt : order) {
+      if (nt % G != 0) continue;
+      const int64_t w = busiest_cu_waves(a, G, nt);
+      if (best_w < 0 || w < best_w) {
+        best_w = w;
+        best = nt;
+      }
+    }
   }
-  return launch_ssm_g<T, MODE, KPL, G, PF, 256, 1>(a, s);
+  switch (best) {
+    case 768: return launch_ssm_g<T, MODE, KPL, G, PF, 768, 1>(a, s);
+    case 1024: return launch_ssm_g<T, MODE, KPL, G, PF, 1024, 1>(a, s);
+    case 512: return launch_ssm_g<T, MODE, KPL, G, PF, 512, 1>(a, s);
+    default: return launch_ssm_g<T, MODE, KPL, G, PF, 256, 1>(a, s);
+  }
 }
 
 template <typename T, int MODE, int KPL>
