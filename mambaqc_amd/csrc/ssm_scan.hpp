@@ -371,8 +371,11 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
 
   Step<T, MODE, KPL> ring[PF];
   const int t_last = Tn - 1;
+  // Slots past the last step are never consumed: a short walk (a decode step
+  // has T = 1) loads only its own steps.
 #pragma unroll
-  for (int i = 0; i < PF; ++i) load_step(ring[i], i < Tn ? i : t_last);
+  for (int i = 0; i < PF; ++i)
+    if (i < Tn) load_step(ring[i], i);
 
   const bool writer = gvalid && (G < 4 || j < 4);
   const int64_t rowY = a.Dm * 4;
