@@ -444,11 +444,13 @@ def lm_timing(args):
         f"{B * T / ms * 1e3:.0f} tokens/s")
     # Recurrent decoding after the 2048-token prompt: one step per new token
     # (the reference re-runs the whole sequence instead).
+    # The decode step as generate() runs it: fed back tokens are sampled in
+    # range, so the step skips the id check (a host round trip per step).
     with torch.inference_mode():
         _, states = lm.forward_with_state(ids)
         tok = ids[:, -1:]
-        lm.forward_with_state(tok, states)
-        dec_ms = event_time_ms(lambda: lm.forward_with_state(tok, states), 20)
+        lm._forward_with_state(tok, states)
+        dec_ms = event_time_ms(lambda: lm._forward_with_state(tok, states), 20)
     log(f"config 5 recurrent decode: {dec_ms:.2f} ms per step of {B} tokens")
     del lm, states
     torch.cuda.empty_cache()
@@ -516,7 +518,7 @@ def run_kernel_loop(args):
             ids = torch.randint(0, 10000, (B, 64), generator=g, device="cuda")
             _, states = lm.forward_with_state(ids)
             tok = ids[:, -1:]
-            fn = lambda: lm.forward_with_state(tok, states)
+            fn = lambda: lm._forward_with_state(tok, states)
             nbytes = sum(p.numel() * p.element_size() for p in lm.parameters())
         elif args.mode == "train":
             # Config 4: block forward + backward under fp16 autocast, loss

@@ -94,6 +94,14 @@ class QuaternionMamba2(nn.Module):
         """Logits of input_ids continuing from per-layer recurrent states
         (None = start of sequence); returns (logits, new_states)."""
         self._check_ids(input_ids)
+        return self._forward_with_state(input_ids, states)
+
+    def _forward_with_state(self, input_ids: torch.Tensor, states=None):
+        """forward_with_state without the id range check. The check reads the ids
+        back to the host (two .item() calls), which stalls the host until the GPU
+        has drained its queue; generate() feeds back tokens it sampled itself,
+        which are in range by construction, so its decode steps skip it and the
+        host stays ahead of the GPU."""
         x = self.dropout(self.embedding(input_ids))
         new_states = []
         for i, layer in enumerate(self.layers):
@@ -128,7 +136,7 @@ class QuaternionMamba2(nn.Module):
             token = torch.multinomial(torch.softmax(nxt, dim=-1), num_samples=1)
             input_ids = torch.cat([input_ids, token], dim=1)
             if step + 1 < max_new_tokens:
-                logits, states = self.forward_with_state(token, states)
+                logits, states = self._forward_with_state(token, states)
         return input_ids
 
     def get_num_params(self, non_embedding: bool = True) -> int:
