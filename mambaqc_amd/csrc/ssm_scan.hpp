@@ -78,32 +78,6 @@ struct Raw : RawBits<N * (int)sizeof(T)> {
   static constexpr int W = (N * (int)sizeof(T) + 3) / 4;
 };
 
-// Load N elements from a byte address (base + 32-bit lane offset).
-template <typename T, int N>
-__device__ inline void raw_load(const char* __restrict__ p, Raw<T, N>& r) {
-  constexpr int W = Raw<T, N>::W;
-  constexpr int bytes = N * (int)sizeof(T);
-  if constexpr (bytes % 16 == 0) {
-#pragma unroll
-    for (int i = 0; i < W / 4; ++i) {
-      uint4 v = reinterpret_cast<const uint4*>(p)[i];
-      r.w[4 * i + 0] = v.x;
-      r.w[4 * i + 1] = v.y;
-      r.w[4 * i + 2] = v.z;
-      r.w[4 * i + 3] = v.w;
-    }
-  } else if constexpr (bytes == 8) {
-    uint2 v = *reinterpret_cast<const uint2*>(p);
-    r.w[0] = v.x;
-    r.w[1] = v.y;
-  } else if constexpr (bytes == 4) {
-    r.w[0] = *reinterpret_cast<const uint32_t*>(p);
-  } else {
-    static_assert(bytes == 2, "unsupported raw width");
-    r.h = *reinterpret_cast<const uint16_t*>(p);
-  }
-}
-
 // Buffer resource over memory from p on: raw (unswizzled), stride 0, the
 // maximum record count, gfx9's 32-bit data-format word. Loads through it take
 // a scalar base (rebuilt per step from SGPRs) plus a 32-bit per-lane offset in
