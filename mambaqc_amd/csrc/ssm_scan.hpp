@@ -345,11 +345,6 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
 
   Step<T, MODE, KPL> ring[PF];
   const int t_last = Tn - 1;
-  // Slots past the last step are never consumed: a short walk (a decode step
-  // has T = 1) loads only its own steps.
-#pragma unroll
-  for (int i = 0; i < PF; ++i)
-    if (i < Tn) load_step(ring[i], i);
 
   const bool writer = gvalid && (G < 4 || j < 4);
   const int64_t rowY = a.Dm * 4;
@@ -360,82 +355,121 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   int next_ckpt = a.h_ckpt ? (ckpt_every < Tn ? ckpt_every - 1 : Tn - 1) : -1;
   int64_t ckpt_idx = 0;
 
-  for (int t0 = 0; t0 < Tn; t0 += PF) {
+  // One step t from ring slot cur.
+  auto walk_step = [&](auto refill, Step<T, MODE, KPL>& cur, int t) {
+    constexpr bool REFILL = decltype(refill)::value;
+    quat acc{0.f, 0.f, 0.f, 0.f};
+    float sv = 0.f;
+    float Sv[4] = {0.f, 0.f, 0.f, 0.f};
+    float Dv = 0.f;
+    if constexpr (MODE == MODE_DL) {
+      const float dl = raw_get(cur.delta, 0);
+      sv = raw_get(cur.s, 0);
+      const float dl2 = dl * dl;
 #pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const int t = t0 + i;
-      if (t >= Tn) break;
-      Step<T, MODE, KPL>& cur = ring[i];
+      for (int kk = 0; kk < KPL; ++kk) {
+        const quat qd = cayley_step(dl, dl2, lam[kk], a.eps);
+        h[kk] = state_step(qd, h[kk], sv, raw_quat(cur.B, kk));
+        qmul_acc(acc, raw_quat(cur.C, kk), h[kk]);
+      }
+    } else {
+      const quat Sq = raw_quat(cur.S, 0);
+      Sv[0] = Sq.w; Sv[1] = Sq.x; Sv[2] = Sq.y; Sv[3] = Sq.z;
+      Dv = raw_get(cur.D, 0);
+#pragma unroll
+      for (int kk = 0; kk < KPL; ++kk) {
+        const quat qk = raw_quat(cur.q, kk);
+        quat hn = qmul(raw_quat(cur.B, kk), Sq);
+        qmul_acc(hn, qk, h[kk]);
+        h[kk] = hn;
+        qmul_acc(acc, raw_quat(cur.C, kk), hn);
+      }
+    }
+    // Refill the consumed slot with step t + PF (clamped: the last group
+    // re-reads the last step, which keeps the loads unconditional).
+    if constexpr (REFILL) {
+      const int tn = t + PF;
+      load_step(cur, tn < Tn ? tn : t_last);
+    }
+    if constexpr (!FULL) {
+      if (!kvalid) acc = quat{0.f, 0.f, 0.f, 0.f};
+    }
 
-      quat acc{0.f, 0.f, 0.f, 0.f};
-      float sv = 0.f;
-      float Sv[4] = {0.f, 0.f, 0.f, 0.f};
-      float Dv = 0.f;
+    float v[4];
+    int c0;
+    const int nc = group_reduce<G>(acc, lane, v, c0);
+    if (writer) {
+      const __amdgpu_buffer_rsrc_t ry = buf_rsrc((T*)a.y + (b * Tn + t) * rowY);
       if constexpr (MODE == MODE_DL) {
-        const float dl = raw_get(cur.delta, 0);
-        sv = raw_get(cur.s, 0);
-        const float dl2 = dl * dl;
-#pragma unroll
-        for (int kk = 0; kk < KPL; ++kk) {
-          const quat qd = cayley_step(dl, dl2, lam[kk], a.eps);
-          h[kk] = state_step(qd, h[kk], sv, raw_quat(cur.B, kk));
-          qmul_acc(acc, raw_quat(cur.C, kk), h[kk]);
-        }
+        if (c0 == 0) v[0] = fmaf(dskip, sv, v[0]);
       } else {
-        const quat Sq = raw_quat(cur.S, 0);
-        Sv[0] = Sq.w; Sv[1] = Sq.x; Sv[2] = Sq.y; Sv[3] = Sq.z;
-        Dv = raw_get(cur.D, 0);
-#pragma unroll
-        for (int kk = 0; kk < KPL; ++kk) {
-          const quat qk = raw_quat(cur.q, kk);
-          quat hn = qmul(raw_quat(cur.B, kk), Sq);
-          qmul_acc(hn, qk, h[kk]);
-          h[kk] = hn;
-          qmul_acc(acc, raw_quat(cur.C, kk), hn);
-        }
-      }
-      // Refill the consumed slot with step t + PF (clamped: the tail re-reads
-      // the last step, which keeps the loads unconditional).
-      {
-        const int tn = t + PF;
-        load_step(cur, tn < Tn ? tn : t_last);
-      }
-      if constexpr (!FULL) {
-        if (!kvalid) acc = quat{0.f, 0.f, 0.f, 0.f};
-      }
-
-      float v[4];
-      int c0;
-      const int nc = group_reduce<G>(acc, lane, v, c0);
-      if (writer) {
-        const __amdgpu_buffer_rsrc_t ry = buf_rsrc((T*)a.y + (b * Tn + t) * rowY);
-        if constexpr (MODE == MODE_DL) {
-          if (c0 == 0) v[0] = fmaf(dskip, sv, v[0]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (e < nc) v[e] = fmaf(Dv, Sv[c0 + e], v[e]);
-        }
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (e < nc) store_elem_buf<T>(ry, offY + (uint32_t)((c0 + e) * (int)sizeof(T)), v[e]);
+          if (e < nc) v[e] = fmaf(Dv, Sv[c0 + e], v[e]);
       }
-      if (a.h_ckpt && t == next_ckpt) {
-        // Chunk t / ckpt_every ends here (or the sequence does).
-        if (gvalid && kvalid) {
-          float e[4 * KPL];
 #pragma unroll
-          for (int kk = 0; kk < KPL; ++kk) {
-            e[4 * kk + 0] = h[kk].w; e[4 * kk + 1] = h[kk].x;
-            e[4 * kk + 2] = h[kk].y; e[4 * kk + 3] = h[kk].z;
-          }
-          store_vec<float, 4 * KPL>(a.h_ckpt + (((b * n_ckpt + ckpt_idx) * a.Dm + d) * a.S + k0) * 4, e);
-        }
-        ++ckpt_idx;
-        next_ckpt = next_ckpt + ckpt_every < Tn ? next_ckpt + ckpt_every : Tn - 1;
-      }
-      if constexpr (SYNC == 1) __syncthreads();
+      for (int e = 0; e < 4; ++e)
+        if (e < nc) store_elem_buf<T>(ry, offY + (uint32_t)((c0 + e) * (int)sizeof(T)), v[e]);
     }
+    if (a.h_ckpt && t == next_ckpt) {
+      // Chunk t / ckpt_every ends here (or the sequence does).
+      if (gvalid && kvalid) {
+        float e[4 * KPL];
+#pragma unroll
+        for (int kk = 0; kk < KPL; ++kk) {
+          e[4 * kk + 0] = h[kk].w; e[4 * kk + 1] = h[kk].x;
+          e[4 * kk + 2] = h[kk].y; e[4 * kk + 3] = h[kk].z;
+        }
+        store_vec<float, 4 * KPL>(a.h_ckpt + (((b * n_ckpt + ckpt_idx) * a.Dm + d) * a.S + k0) * 4, e);
+      }
+      ++ckpt_idx;
+      next_ckpt = next_ckpt + ckpt_every < Tn ? next_ckpt + ckpt_every : Tn - 1;
+    }
+    if constexpr (SYNC == 1) __syncthreads();
+  };
+
+  // Whole groups of PF steps run in a loop with no exit inside the group and
+  // an unconditional prologue, so every path into the loop head has issued all
+  // PF steps' loads in order: the wait for slot 0 leaves the later slots in
+  // flight. (An exit inside the group, or prologue loads under conditions,
+  // make the compiler assume at the loop head that slot 0 was loaded last,
+  // and wait for every load in flight once per group.) The remaining steps,
+  // and all of a walk shorter than PF, run in one guarded tail.
+  //
+  // Lanes that load 8 bytes of B and C per step (one 16-bit state) keep the
+  // ring in flight across groups: measured at T 2048, D 1536, S 64 (bf16),
+  // batch 1 1.00 -> 0.89 ms and batch 2 1.34 -> 1.25 ms. Lanes that load 16
+  // bytes still wait for all their loads once per group, which measured
+  // 0.5-1.5 % faster at the config-3 shape (B4 T2048 D1536 S64) than keeping
+  // PF steps in flight, and the same with 4 or 6 steps.
+  constexpr bool DRAIN = KPL * 4 * sizeof(T) >= 16;
+  // s_waitcnt vmcnt(0) with expcnt and lgkmcnt at their maxima (gfx9 fields:
+  // vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in bits [15:14]).
+  constexpr int kWaitVm0 = 0x0F70;
+  int t0 = 0;
+  if (Tn >= PF) {
+    // The scheduling barriers keep the prologue's loads in slot order.
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      load_step(ring[i], i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (; t0 + PF <= Tn; t0 += PF) {
+      if constexpr (DRAIN) __builtin_amdgcn_s_waitcnt(kWaitVm0);
+#pragma unroll
+      for (int i = 0; i < PF; ++i) walk_step(std::true_type{}, ring[i], t0 + i);
+      if constexpr (SYNC == 2) __syncthreads();
+    }
+  } else {
+    // A walk shorter than PF (a decode step has T = 1) loads only its steps.
+#pragma unroll
+    for (int i = 0; i < PF; ++i)
+      if (i < Tn) load_step(ring[i], i);
+  }
+  if (t0 < Tn) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i)
+      if (t0 + i < Tn) walk_step(std::false_type{}, ring[i], t0 + i);
     if constexpr (SYNC == 2) __syncthreads();
   }
 
