@@ -71,27 +71,43 @@ struct SsmBwdArgs {
 
 // Pull dq back through q = Cayley(dl * Lambda) (closed form, see ssm_scan.hpp):
 //   N = 1 - dl a + dl^2 n2 (clamped below at eps), P = 1 - dl^2 n2,
-//   q0 = P / N,  qv = dl v / N.
-// r = 1 / max(N, eps) and live = (N > eps) come from the state recompute.
-// Returns d dl; accumulates the gradients w.r.t. a and v into da, dv. When the
-// clamp engages N is constant, as in the reference's clamp_min.
-__device__ inline float cayley_pullback(const quat& g, const quat& q, float dl, float dl2,
-                                        float r, bool live, const LamConst& L, float& da,
-                                        float (&dv)[3]) {
-  const float gq = g.w * q.w + g.x * q.x + g.y * q.y + g.z * q.z;   // <dq, q>
-  const float gv = g.x * L.v0 + g.y * L.v1 + g.z * L.v2;            // <dq_vec, v>
-  const float gql = live ? gq : 0.f;
-  // d/d dl: dP = -2 dl n2, dN = -a + 2 dl n2
-  const float ddl = (g.w * (-2.f * dl * L.n2) + gv - gql * fmaf(2.f * dl, L.n2, -L.a)) * r;
-  // d/da: dP = -dl^2 a / 2, dN = -dl + dl^2 a / 2
-  const float h = 0.5f * dl2;
-  da += (g.w * (-h * L.a) - gql * fmaf(h, L.a, -dl)) * r;
-  // d/dv_i: dP = -dl^2 v_i / 2, dN = dl^2 v_i / 2, d(dl v_j) = dl [i == j]
-  const float cv = -h * (g.w + gql);
-  dv[0] += fmaf(cv, L.v0, dl * g.x) * r;
-  dv[1] += fmaf(cv, L.v1, dl * g.y) * r;
-  dv[2] += fmaf(cv, L.v2, dl * g.z) * r;
+//   q0 = P / N,  qv = dl v / N,  n2 = (a^2 + |v|^2) / 4.
+// With r = 1 / max(N, eps), cq = dl r, gq = <dq, q> (taken as 0 where the clamp
+// engaged: N is then constant, as in the reference's clamp_min) and
+// u = dq.w + gq:
+//   d dl  = r (<dq_vec, v> + a gq - 2 dl n2 u)
+//   d a   = r (dl gq - (dl^2 / 2) a u)      = cq gq - a (cq dl u) / 2
+//   d v_i = r (dl dq_i - (dl^2 / 2) v_i u)  = cq dq_i - v_i (cq dl u) / 2
+// The terms that do not involve a or v are summed over t in PullAcc and
+// combined with a and v once, after the walk (pull_finish).
+struct PullAcc {
+  float da = 0.f, dv[3] = {0.f, 0.f, 0.f}, sx = 0.f;
+};
+
+// LIVE: the clamp is known not to have engaged (live is then ignored).
+template <bool LIVE>
+__device__ inline float cayley_pullback(const quat& g, float qw, float cq, float dl, float r,
+                                        bool live, const LamConst& L, PullAcc& acc) {
+  const float gv = g.x * L.v0 + g.y * L.v1 + g.z * L.v2;  // <dq_vec, v>
+  float gq = fmaf(g.w, qw, cq * gv);                        // <dq, q>
+  if constexpr (!LIVE) gq = live ? gq : 0.f;
+  const float u = g.w + gq;
+  const float ddl = fmaf(dl * (-2.f * L.n2), u, fmaf(L.a, gq, gv)) * r;
+  acc.sx = fmaf(cq * dl, u, acc.sx);
+  acc.da = fmaf(cq, gq, acc.da);
+  acc.dv[0] = fmaf(cq, g.x, acc.dv[0]);
+  acc.dv[1] = fmaf(cq, g.y, acc.dv[1]);
+  acc.dv[2] = fmaf(cq, g.z, acc.dv[2]);
   return ddl;
+}
+
+// The gradients w.r.t. a and v from the sums of cayley_pullback.
+__device__ inline void pull_finish(const PullAcc& acc, const LamConst& L, float& da, float (&dv)[3]) {
+  const float hs = 0.5f * acc.sx;
+  da = fmaf(-L.a, hs, acc.da);
+  dv[0] = fmaf(-L.v0, hs, acc.dv[0]);
+  dv[1] = fmaf(-L.v1, hs, acc.dv[1]);
+  dv[2] = fmaf(-L.v2, hs, acc.dv[2]);
 }
 
 __device__ inline quat qconj(const quat& q) { return quat{q.w, -q.x, -q.y, -q.z}; }
@@ -126,11 +142,13 @@ __device__ inline void group_reduce2(float& u, float& w, int lane) {
 }
 
 // SYNC: a block barrier after every chunk keeps the block's waves on the same
-// chunk. Unlike the forward, the backward gains nothing from it: it is VALU
-// bound (about 215 VALU instructions per step and lane at bf16 and G = 64,
-// against 5 ms of HBM traffic at config 3), so the launcher runs free 256-thread
-// blocks, measured 4 % faster than lockstep 768-thread ones. Double-buffering
-// the chunk operands was measured too and gave nothing at K = 8.
+// chunk. Unlike the forward, the backward gains nothing from it: about half of
+// its traffic is writes (dB, dC), and it moves its bytes at about the rate of a
+// plain device copy (4.6-4.7 TB/s at config 3, where a 1 GiB copy runs at
+// 4.7-5.3), so the launcher runs free 256-thread blocks, measured 4 % faster
+// than lockstep 768-thread ones. Its VALU work (about 160 instructions per step
+// and lane at 16-bit storage and G = 64) takes about 3.5 ms of the 5.9.
+// Double-buffering the chunk operands was measured too and gave nothing at K = 8.
 // WPE caps the registers at two waves per SIMD (<= 256 VGPRs): left alone the
 // compiler takes 276 (one wave per SIMD); at three waves per SIMD it spills to
 // scratch and runs twice as slow.
@@ -168,7 +186,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
   const LamConst L = lam_const(a.lam_alpha, a.lam_imag, dk);
   const float Dv = a.dvec[d];
 
-  float da = 0.f, dv[3] = {0.f, 0.f, 0.f}, dD = 0.f;
+  PullAcc pacc;
+  float dD = 0.f;
   quat carry{0.f, 0.f, 0.f, 0.f};
   if (a.dh_last) {
     float e[4];
@@ -222,7 +241,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
     const __amdgpu_buffer_rsrc_t rdd = buf_rsrc((char*)a.d_delta + row0 * (int64_t)stepF);
     const __amdgpu_buffer_rsrc_t rds = buf_rsrc((char*)a.d_s + row0 * (int64_t)stepF);
     quat hs[K + 1];
-    float rq[K];  // 1 / max(N, eps) of each step, negated where the clamp engaged
+    float rq[K];  // 1 / max(N, eps) of each step
     if (c > 0) {
       hs[0] = quat{o.h_in.x, o.h_in.y, o.h_in.z, o.h_in.w};
     } else if (a.h0) {
@@ -232,7 +251,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
     } else {
       hs[0] = quat{0.f, 0.f, 0.f, 0.f};
     }
-    // Recompute the chunk's states (the forward's arithmetic).
+    // Recompute the chunk's states (the forward's arithmetic). `clamped` marks
+    // the wave's lanes in which the eps clamp engaged at some step (wave-uniform).
+    uint64_t clamped = 0;
 #pragma unroll
     for (int i = 0; i < K; ++i) {
       if (FULLC || i < len) {
@@ -240,58 +261,70 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
         const float dl2 = dl * dl;
         const float Nraw = fmaf(dl2, L.n2, fmaf(-dl, L.a, 1.f));
         const float r = __builtin_amdgcn_rcpf(fmaxf(Nraw, a.eps));
-        rq[i] = Nraw > a.eps ? r : -r;
+        rq[i] = r;
+        clamped |= __builtin_amdgcn_ballot_w64(!(Nraw > a.eps));
         const float cq = dl * r;
         const quat q{fmaf(-dl2, L.n2, 1.f) * r, cq * L.v0, cq * L.v1, cq * L.v2};
         hs[i + 1] = state_step(q, hs[i], raw_get(o.rs[i], 0), raw_quat(o.rB[i], 0));
       }
     }
-    // Adjoint steps, last to first.
+    // Adjoint steps, last to first. LIVE: no lane of the wave hit the clamp in
+    // this chunk (the usual case: in the block N >= 1, as delta >= 0 and a < 0).
+    auto adjoint = [&](auto all_live) {
+      constexpr bool LIVE = decltype(all_live)::value;
 #pragma unroll
-    for (int i = K - 1; i >= 0; --i) {
-      if (FULLC || i < len) {
-        const float dl = raw_get(o.rd[i], 0);
-        const float dl2 = dl * dl;
-        const float sv = raw_get(o.rs[i], 0);
-        const float r = fabsf(rq[i]);
-        const float cq = dl * r;
-        const quat q{fmaf(-dl2, L.n2, 1.f) * r, cq * L.v0, cq * L.v1, cq * L.v2};
-        const quat gy = raw_quat(o.rg[i], 0);
-        const quat Ck = raw_quat(o.rC[i], 0);
-        const quat Bk = raw_quat(o.rB[i], 0);
-        quat g = carry;
-        qmul_acc(g, qconj(Ck), gy);
-        quat dq{0.f, 0.f, 0.f, 0.f};
-        qmul_acc(dq, g, qconj(hs[i]));
-        quat dC{0.f, 0.f, 0.f, 0.f};
-        qmul_acc(dC, gy, qconj(hs[i + 1]));
-        float ddl = cayley_pullback(dq, q, dl, dl2, r, rq[i] > 0.f, L, da, dv);
-        float dsk = g.w * Bk.w + g.x * Bk.x + g.y * Bk.y + g.z * Bk.z;
-        carry = quat{0.f, 0.f, 0.f, 0.f};
-        qmul_acc(carry, qconj(q), g);
-        if (own) {
-          const float eB[4] = {sv * g.w, sv * g.x, sv * g.y, sv * g.z};
-          const float eC[4] = {dC.w, dC.x, dC.y, dC.z};
-          store_quat_buf<T>(rdB, offBC, eB, (uint32_t)i * stepBC);
-          store_quat_buf<T>(rdC, offBC, eC, (uint32_t)i * stepBC);
-        } else {
-          ddl = 0.f;
-          dsk = 0.f;
-        }
-        group_reduce2<G>(ddl, dsk, lane);
-        // Lane 0 holds the d delta total and lane 1 the ds total; one DPP read
-        // brings the latter to lane 0, which stores both. (Stores from two
-        // lanes under different conditions get merged by the compiler into
-        // one store whose buffer descriptor is lane-dependent, which costs a
-        // waterfall loop.)
-        const float ds_tot = G > 1 ? lane_xor1(dsk) : dsk;
-        if (gvalid && j == 0) {
-          store_elem_buf<float>(rdd, offF, ddl, (uint32_t)i * stepF);
-          store_elem_buf<float>(rds, offF, fmaf(Dv, gy.w, ds_tot), (uint32_t)i * stepF);
-          dD = fmaf(gy.w, sv, dD);
+      for (int i = K - 1; i >= 0; --i) {
+        if (FULLC || i < len) {
+          const float dl = raw_get(o.rd[i], 0);
+          const float dl2 = dl * dl;
+          const float sv = raw_get(o.rs[i], 0);
+          const float r = rq[i];
+          const float cq = dl * r;
+          const float qw = fmaf(-dl2, L.n2, 1.f) * r;
+          const quat q{qw, cq * L.v0, cq * L.v1, cq * L.v2};
+          bool live = true;
+          if constexpr (!LIVE) live = fmaf(dl2, L.n2, fmaf(-dl, L.a, 1.f)) > a.eps;
+          const quat gy = raw_quat(o.rg[i], 0);
+          const quat Ck = raw_quat(o.rC[i], 0);
+          const quat Bk = raw_quat(o.rB[i], 0);
+          quat g = carry;
+          qmul_acc(g, qconj(Ck), gy);
+          quat dq{0.f, 0.f, 0.f, 0.f};
+          qmul_acc(dq, g, qconj(hs[i]));
+          quat dC{0.f, 0.f, 0.f, 0.f};
+          qmul_acc(dC, gy, qconj(hs[i + 1]));
+          float ddl = cayley_pullback<LIVE>(dq, qw, cq, dl, r, live, L, pacc);
+          float dsk = g.w * Bk.w + g.x * Bk.x + g.y * Bk.y + g.z * Bk.z;
+          carry = quat{0.f, 0.f, 0.f, 0.f};
+          qmul_acc(carry, qconj(q), g);
+          if (own) {
+            const float eB[4] = {sv * g.w, sv * g.x, sv * g.y, sv * g.z};
+            const float eC[4] = {dC.w, dC.x, dC.y, dC.z};
+            store_quat_buf<T>(rdB, offBC, eB, (uint32_t)i * stepBC);
+            store_quat_buf<T>(rdC, offBC, eC, (uint32_t)i * stepBC);
+          } else {
+            ddl = 0.f;
+            dsk = 0.f;
+          }
+          group_reduce2<G>(ddl, dsk, lane);
+          // Lane 0 holds the d delta total and lane 1 the ds total; one DPP read
+          // brings the latter to lane 0, which stores both. (Stores from two
+          // lanes under different conditions get merged by the compiler into
+          // one store whose buffer descriptor is lane-dependent, which costs a
+          // waterfall loop.)
+          const float ds_tot = G > 1 ? lane_xor1(dsk) : dsk;
+          if (gvalid && j == 0) {
+            store_elem_buf<float>(rdd, offF, ddl, (uint32_t)i * stepF);
+            store_elem_buf<float>(rds, offF, fmaf(Dv, gy.w, ds_tot), (uint32_t)i * stepF);
+            dD = fmaf(gy.w, sv, dD);
+          }
         }
       }
-    }
+    };
+    if (clamped == 0)
+      adjoint(std::true_type{});
+    else
+      adjoint(std::false_type{});
     if constexpr (SYNC) __syncthreads();
   };
 
@@ -315,6 +348,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
       const float e[4] = {carry.w, carry.x, carry.y, carry.z};
       store_vec<T, 4>((T*)a.dh0 + sidx, e);
     }
+    float da, dv[3];
+    pull_finish(pacc, L, da, dv);
     // Chain to the raw parameters: a = -softplus(alpha), v = tanh(imag).
     const float alpha = a.lam_alpha[dk];
     const float sig = alpha > 20.f ? 1.f : 1.f / (1.f + expf(-alpha));

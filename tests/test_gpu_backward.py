@@ -117,6 +117,40 @@ def test_ssm_dl_backward_without_state_terms():
         assert_close(a.grad, r.grad, 1e-4, name)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_ssm_dl_backward_clamp_engaged(dtype):
+    """Steps where the Cayley denominator's squared norm N falls below eps, so
+    q = conj(den) (x) num / eps with N held constant (the reference's
+    clamp_min). A large eps keeps those steps well conditioned; negative deltas
+    at two steps put most lanes below it there while the other steps and
+    chunks stay above."""
+    b, T, d, k = 2, 11, 6, 8
+    eps = 0.5
+    ins = _dl_inputs(b, T, d, k, seed=5, dtype=dtype)
+    ins[0][:, 3] = -1.6
+    ins[0][1, 7] = -1.2
+    # The clamp must engage at those steps for some lanes and not for others.
+    a = -torch.nn.functional.softplus(ins[4].double())
+    v = torch.tanh(ins[5].double())
+    dl = ins[0].double()[..., None]
+    N = 1 - dl * a + dl ** 2 * (a ** 2 + (v ** 2).sum(-1)) / 4
+    assert (N[:, 3] < eps).any() and (N[:, 3] > eps).any()
+    assert (N[:, :3] > eps).all() and (N[0, 4:] > eps).all()
+    g = torch.Generator().manual_seed(9)
+    gy = torch.randn(b, T, d, 4, generator=g).to(dtype)
+
+    got_in = [_leaf(t, DEV) for t in ins]
+    y = K.ssm_forward_fused_dl(*got_in, eps=eps)
+    (y.float() * gy.to(DEV).float()).sum().backward()
+    ref_in = [_leaf(t.double()) for t in ins]
+    yr = oracle.ssm_forward_dl_reference(*ref_in, eps=eps)
+    (yr * gy.double()).sum().backward()
+
+    assert_close(y, yr, tol(dtype), f"y {dtype}")
+    for a_, r_, name in zip(got_in, ref_in, ["delta", "s", "B", "C", "la", "li", "D"]):
+        assert_close(a_.grad, r_.grad, tol(dtype), f"{name} {dtype}")
+
+
 def test_ssm_dl_backward_config3_slices():
     """Config-3 sizes in bf16 (B4 T2048 D1536 S64): lanes are independent, so the
     per-(b, t, d) gradients of d-slices are checked against the oracle on the
