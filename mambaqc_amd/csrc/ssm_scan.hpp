@@ -522,15 +522,28 @@ inline int64_t busiest_cu_waves(const SsmArgs& a, int G, int NT) {
   return (blocks + kCUs - 1) / kCUs * (NT / 64);
 }
 
+// The largest block whose lanes get the kernel's registers without spilling
+// to scratch (NT threads leave 512 / (NT / 256) VGPRs per lane), from the
+// register counts of the compiled kernels: the materialised-q form carries
+// q, S and D in the ring besides B and C, and four states per lane carry twice
+// the operands of two.
+template <typename T, int MODE, int KPL>
+constexpr int ssm_max_threads() {
+  if constexpr (MODE == MODE_DL) return KPL <= 2 ? 1024 : (sizeof(T) == 2 ? 768 : 512);
+  if constexpr (sizeof(T) == 2) return KPL == 1 ? 1024 : 768;
+  return KPL <= 2 ? 768 : 256;
+}
+
 template <typename T, int MODE, int KPL, int G>
 int launch_ssm_shape(const SsmArgs& a, hipStream_t s) {
   constexpr int PF = ssm_prefetch<T, KPL>();
+  constexpr int kMaxNT = ssm_max_threads<T, MODE, KPL>();
   int best = 256;
   if constexpr (G <= 64) {
     const int order[4] = {768, 1024, 512, 256};
     int64_t best_w = -1;
     for (int nt : order) {
-      if (nt % G != 0) continue;
+      if (nt % G != 0 || nt > kMaxNT) continue;
       const int64_t w = busiest_cu_waves(a, G, nt);
       if (best_w < 0 || w < best_w) {
         best_w = w;
@@ -539,11 +552,19 @@ int launch_ssm_shape(const SsmArgs& a, hipStream_t s) {
     }
   }
   switch (best) {
-    case 768: return launch_ssm_g<T, MODE, KPL, G, PF, 768, 1>(a, s);
-    case 1024: return launch_ssm_g<T, MODE, KPL, G, PF, 1024, 1>(a, s);
-    case 512: return launch_ssm_g<T, MODE, KPL, G, PF, 512, 1>(a, s);
-    default: return launch_ssm_g<T, MODE, KPL, G, PF, 256, 1>(a, s);
+    case 768:
+      if constexpr (kMaxNT >= 768) return launch_ssm_g<T, MODE, KPL, G, PF, 768, 1>(a, s);
+      break;
+    case 1024:
+      if constexpr (kMaxNT >= 1024) return launch_ssm_g<T, MODE, KPL, G, PF, 1024, 1>(a, s);
+      break;
+    case 512:
+      if constexpr (kMaxNT >= 512) return launch_ssm_g<T, MODE, KPL, G, PF, 512, 1>(a, s);
+      break;
+    default:
+      break;
   }
+  return launch_ssm_g<T, MODE, KPL, G, PF, 256, 1>(a, s);
 }
 
 template <typename T, int MODE, int KPL>
