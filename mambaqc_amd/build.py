@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -40,17 +41,60 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found: set HIPCC or install ROCm under /opt/rocm")
 
 
+# The compiler reports each kernel's register and scratch use as remarks.
+RESOURCE_REMARKS = "-Rpass-analysis=kernel-resource-usage"
+_FN = re.compile(r"remark: Function Name: (\S+)")
+_SCRATCH = re.compile(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)")
+_QUOTED = re.compile(r"^\s*(\d+\s*)?\|")  # source lines quoted under a remark
+
+
+def _spilling_kernels(stderr: str) -> list[str]:
+    """Kernels whose resource remarks show scratch memory (register spills)."""
+    out, name = [], None
+    for line in stderr.splitlines():
+        m = _FN.search(line)
+        if m:
+            name = m.group(1)
+            continue
+        m = _SCRATCH.search(line)
+        if m and name is not None and int(m.group(1)) > 0:
+            out.append(f"{name} ({m.group(1)} bytes/lane)")
+    return out
+
+
 def _compile(hipcc: str, src: Path, obj: Path) -> None:
-    cmd = [hipcc, *HIPFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *HIPFLAGS, RESOURCE_REMARKS, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # The host pass does not know the packed-fp32 feature and says so; that
-    # warning is expected and filtered from the log.
+    # warning is expected and filtered from the log, as are the resource
+    # remarks (and the source lines the compiler quotes under them).
     noise = "'-packed-fp32-ops' is not a recognized feature"
-    err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)
+    lines, includes, in_remark = [], [], False
+    for l in r.stderr.splitlines():
+        if noise in l:
+            continue
+        if l.startswith("In file included from"):
+            includes.append(l)
+            continue
+        if "[-Rpass-analysis=kernel-resource-usage]" in l:
+            includes, in_remark = [], True
+            continue
+        if in_remark and _QUOTED.match(l):
+            continue
+        in_remark = False
+        lines += includes + [l]
+        includes = []
+    err = "\n".join(lines + includes)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{err}")
     if err.strip():
         print(err, file=sys.stderr)
+    # Every kernel here is written to run from registers; scratch means a
+    # launch shape or template instance outgrew its register budget.
+    spills = _spilling_kernels(r.stderr)
+    if spills:
+        raise RuntimeError(f"{src.name}: kernels spill registers to scratch:\n  " +
+                           "\n  ".join(spills))
 
 
 def build(verbose: bool = True) -> Path:

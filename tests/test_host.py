@@ -236,3 +236,23 @@ def test_param_f32_cache():
     with torch.inference_mode():
         r = torch.randn(3, 2).bfloat16()
         assert torch.equal(nat.param_f32(r), r.float())
+
+
+def test_build_rejects_kernels_that_spill():
+    """The build reads the compiler's per-kernel resource remarks and refuses a
+    kernel with scratch memory (a register spill): the parser finds the one
+    kernel of a remark log that has scratch and none of those that have none."""
+    from mambaqc_amd import build as B
+    log = "\n".join([
+        "In file included from x.hip:2:",
+        "x.hpp:10:1: remark: Function Name: _Z4fastv [-Rpass-analysis=kernel-resource-usage]",
+        "   10 | __global__ void fast() {",
+        "      | ^",
+        "x.hpp:10:1: remark:     VGPRs: 40 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hpp:10:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hpp:20:1: remark: Function Name: _Z4slowv [-Rpass-analysis=kernel-resource-usage]",
+        "x.hpp:20:1: remark:     VGPRs: 128 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hpp:20:1: remark:     ScratchSize [bytes/lane]: 116 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert B._spilling_kernels(log) == ["_Z4slowv (116 bytes/lane)"]
+    assert B.RESOURCE_REMARKS == "-Rpass-analysis=kernel-resource-usage"
