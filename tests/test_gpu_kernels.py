@@ -183,6 +183,18 @@ def test_ssm_forward_fused(k, dtype):
     assert_close(got, want, tol(dtype), f"ssm_q k={k} {dtype}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_ssm_forward_fused_wide(dtype):
+    """d_inner 2048 at batch 4: the launcher's block size is capped where the
+    materialised-q kernel would spill (several rounds of blocks)."""
+    b, T, d, k = 4, 9, 2048, 64
+    q, Bm, S, C, D = _q_inputs(b, T, d, k, seed=40, dtype=dtype)
+    Dx = D.view(1, 1, d).expand(b, T, d)
+    got = K.ssm_forward_fused(*(t.to(DEV) for t in (q, Bm, S, C)), Dx.to(DEV))
+    want = oracle.ssm_forward_reference(up(q), up(Bm), up(S), up(C), up(Dx))
+    assert_close(got, want, tol(dtype), f"ssm_q wide {dtype}")
+
+
 def test_ssm_forward_fused_strided_D():
     b, T, d, k = 2, 9, 4, 8
     q, Bm, S, C, _ = _q_inputs(b, T, d, k, seed=21, dtype=torch.float32)
@@ -226,8 +238,11 @@ def _dl_inputs(b, T, d, k, seed, dtype):
                                    # hardware block order
                                    (2, 37, 64, 64), (4, 19, 96, 64), (3, 21, 100, 64),
                                    # enough (b, d) for two states per lane in 16-bit storage
-                                   # (>= 12 waves per CU) and 768-thread blocks; d ragged
-                                   (8, 5, 768, 64), (3, 7, 2050, 64)])
+                                   # (>= 12 waves per CU) and 768-thread blocks; d ragged;
+                                   # walks shorter than, equal to and past one group of 8
+                                   # prefetched steps (a tail of 5)
+                                   (8, 5, 768, 64), (3, 7, 2050, 64), (8, 8, 768, 64),
+                                   (8, 21, 768, 64)])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_ssm_fused_dl(shape, dtype):
     a = _dl_inputs(*shape, seed=sum(shape), dtype=dtype)
