@@ -85,7 +85,8 @@ int mqc_cumprod_scan_fwd(const void* q, void* out, int64_t batch, int64_t seq_le
  * D[b*d_sb + t*d_st + d*d_sd] (strides in elements, 0 allowed, so an expanded
  * [d_inner] vector needs no copy); h0: dtype [batch, d_inner, d_state, 4] or
  * NULL for zeros; y: dtype [batch, seq_len, d_inner, 4]; h_last: dtype
- * [batch, d_inner, d_state, 4] or NULL.
+ * [batch, d_inner, d_state, 4] or NULL. With seq_len 0, h_last (if given)
+ * receives h0, or zeros, and the per-step operands may be NULL.
  * Replaces ssm_forward_fused, mambaqc/kernels/ssm_fused.py:340-401, and (with
  * seq_len = 1, h0 = h_prev, h_last = h_new) ssm_step_fused, :258-337. */
 int mqc_ssm_q_fwd(const void* q, const void* B, const void* S, const void* C, const void* D,
@@ -103,7 +104,9 @@ int mqc_ssm_q_fwd(const void* q, const void* B, const void* S, const void* C, co
  * [batch, seq_len, d_inner, d_state, 4]; lambda_alpha: fp32 [d_inner, d_state];
  * lambda_imag: fp32 [d_inner, d_state, 3]; D: fp32 [d_inner]; h0: dtype
  * [batch, d_inner, d_state, 4] or NULL; y: dtype [batch, seq_len, d_inner, 4];
- * h_last: dtype [batch, d_inner, d_state, 4] or NULL.
+ * h_last: dtype [batch, d_inner, d_state, 4] or NULL. With seq_len 0, h_last (if
+ * given) receives h0, or zeros; delta, s, B, C and y may then be NULL, the
+ * parameters may not.
  * Replaces the body of QuaternionMamba2Block._ssm_forward,
  * mambaqc/models/quaternion_mamba2_block.py:206-228 (Lambda, z = delta*Lambda,
  * cayley_discretization_fused, ssm_forward_fused), without materialising z or q. */
@@ -167,7 +170,7 @@ int mqc_ssm_bwd_ckpt_every(int dtype);
 /* mqc_ssm_fused_fwd plus fp32 state checkpoints for the backward:
  * h_ckpt [batch, ceil(seq_len / ckpt_every), d_inner, d_state, 4] receives the
  * state at the last step of every chunk of ckpt_every steps (the last chunk may
- * be shorter). */
+ * be shorter). With seq_len 0 it has no entries and may be NULL. */
 int mqc_ssm_fused_fwd_train(const void* delta, const void* s, const void* B, const void* C,
                             const float* lambda_alpha, const float* lambda_imag, const float* D,
                             const void* h0, void* y, void* h_last, float* h_ckpt,
@@ -183,7 +186,9 @@ int mqc_ssm_fused_fwd_train(const void* delta, const void* s, const void* B, con
  * dlambda_imag_part fp32 [batch, d_inner, d_state, 3], dD_part fp32
  * [batch, d_inner] (the caller sums them over batch), and dh0 (dtype
  * [batch, d_inner, d_state, 4]) if non-NULL. h0 and h_ckpt must be the forward's;
- * ckpt_every must equal mqc_ssm_bwd_ckpt_every(dtype); d_state <= 64. */
+ * ckpt_every must equal mqc_ssm_bwd_ckpt_every(dtype); d_state <= 64. With
+ * seq_len 0 the partials are zeros and dh0 = dh_last (zeros without it); the
+ * per-step tensors and h_ckpt may then be NULL. */
 int mqc_ssm_fused_bwd(const void* delta, const void* s, const void* B, const void* C,
                       const float* lambda_alpha, const float* lambda_imag, const float* D,
                       const void* h0, const float* h_ckpt, int64_t ckpt_every, const void* gy,

@@ -23,18 +23,20 @@ int mqc_ssm_fused_fwd_train(const void* delta, const void* s, const void* B, con
   if (batch < 0 || seq_len < 0 || d_inner < 0 || d_state < 0 || ckpt_every < 1)
     return MQC_E_SHAPE;
   if (dtype != MQC_F32 && dtype != MQC_BF16 && dtype != MQC_F16) return MQC_E_DTYPE;
-  const bool work = batch > 0 && d_inner > 0 && seq_len > 0;
-  if (work && d_state == 0) return MQC_E_SHAPE;
-  if (work && (!delta || !s || !B || !C || !lambda_alpha || !lambda_imag || !D || !y || !h_ckpt))
-    return MQC_E_NULL;
+  // An empty walk (seq_len 0) still writes h_last: h0, or zeros without h0.
+  const bool steps = batch > 0 && d_inner > 0 && seq_len > 0;
+  const bool state_only = batch > 0 && d_inner > 0 && seq_len == 0 && h_last && d_state > 0;
+  if (steps && d_state == 0) return MQC_E_SHAPE;
+  if (steps && (!delta || !s || !B || !C || !y || !h_ckpt)) return MQC_E_NULL;
+  if ((steps || state_only) && (!lambda_alpha || !lambda_imag || !D)) return MQC_E_NULL;
   if (batch > 65535 || d_inner > (1LL << 24) || d_state > 256) return MQC_E_LIMIT;
   if (h_ckpt && !aligned(h_ckpt, 16)) return MQC_E_ALIGN;
   SsmArgs a{};
   a.delta = delta; a.s = s; a.lam_alpha = lambda_alpha; a.lam_imag = lambda_imag; a.dvec = D;
   a.Bm = B; a.Cm = C; a.h0 = h0; a.y = y; a.h_last = h_last;
-  a.h_ckpt = h_ckpt; a.ckpt_every = ckpt_every;
+  a.h_ckpt = steps ? h_ckpt : nullptr; a.ckpt_every = ckpt_every;
   a.batch = batch; a.T = seq_len; a.Dm = d_inner; a.S = d_state; a.eps = eps;
-  if (!work) return MQC_OK;
+  if (!steps && !state_only) return MQC_OK;
   switch (dtype) {
     case MQC_F32: return launch_ssm<float, MODE_DL>(a, (hipStream_t)stream);
     case MQC_BF16: return launch_ssm<bf16_t, MODE_DL>(a, (hipStream_t)stream);
@@ -51,11 +53,15 @@ int mqc_ssm_fused_bwd(const void* delta, const void* s, const void* B, const voi
                       int64_t d_state, float eps, int dtype, void* stream) {
   if (batch < 0 || seq_len < 0 || d_inner < 0 || d_state < 0) return MQC_E_SHAPE;
   if (dtype != MQC_F32 && dtype != MQC_BF16 && dtype != MQC_F16) return MQC_E_DTYPE;
-  const bool work = batch > 0 && d_inner > 0 && seq_len > 0;
-  if (work && d_state == 0) return MQC_E_SHAPE;
-  if (work && (!delta || !s || !B || !C || !lambda_alpha || !lambda_imag || !D || !h_ckpt ||
-               !gy || !d_delta || !d_s || !dB || !dC || !dlambda_alpha_part ||
-               !dlambda_imag_part || !dD_part))
+  // An empty walk (seq_len 0) still writes its outputs: dh0 = dh_last (zeros
+  // without it) and zero parameter partials.
+  const bool steps = batch > 0 && d_inner > 0 && seq_len > 0;
+  const bool empty_walk = batch > 0 && d_inner > 0 && seq_len == 0 && d_state > 0;
+  if (steps && d_state == 0) return MQC_E_SHAPE;
+  if (steps && (!delta || !s || !B || !C || !h_ckpt || !gy || !d_delta || !d_s || !dB || !dC))
+    return MQC_E_NULL;
+  if ((steps || empty_walk) && (!lambda_alpha || !lambda_imag || !D || !dlambda_alpha_part ||
+                                !dlambda_imag_part || !dD_part))
     return MQC_E_NULL;
   if (batch > 65535 || d_inner > (1LL << 24) || d_state > 64) return MQC_E_LIMIT;
   if (ckpt_every != mqc_ssm_bwd_ckpt_every(dtype)) return MQC_E_LIMIT;
@@ -65,7 +71,7 @@ int mqc_ssm_fused_bwd(const void* delta, const void* s, const void* B, const voi
   a.dh_last = dh_last; a.d_delta = d_delta; a.d_s = d_s; a.dB = dB; a.dC = dC;
   a.dalpha_part = dlambda_alpha_part; a.dimag_part = dlambda_imag_part; a.dD_part = dD_part;
   a.dh0 = dh0; a.batch = batch; a.T = seq_len; a.Dm = d_inner; a.S = d_state; a.eps = eps;
-  if (!work) return MQC_OK;
+  if (!steps && !empty_walk) return MQC_OK;
   switch (dtype) {
     case MQC_F32: return launch_ssm_bwd<float>(a, (hipStream_t)stream);
     case MQC_BF16: return launch_ssm_bwd<bf16_t>(a, (hipStream_t)stream);

@@ -329,7 +329,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
   };
 
   Ops buf;
-  {
+  if (nC > 0) {
     const int c = nC - 1;
     const int len = (int)(Tn - c * K);
     load_chunk(buf, c, len);
@@ -384,7 +384,9 @@ int launch_ssm_bwd_g(const SsmBwdArgs& a, hipStream_t s) {
 
 template <typename T>
 int launch_ssm_bwd(const SsmBwdArgs& a, hipStream_t s) {
-  if (a.batch == 0 || a.T == 0 || a.Dm == 0) return MQC_OK;
+  // T == 0 still launches: the walk is empty, dh0 = dh_last and the parameter
+  // partials are zero.
+  if (a.batch == 0 || a.Dm == 0) return MQC_OK;
   // K consecutive steps of one tensor must be addressable with 32-bit offsets.
   if (a.Dm * a.S * 4 * (int64_t)sizeof(T) * ssm_bwd_chunk<T>() >= ((int64_t)1 << 32))
     return MQC_E_LIMIT;

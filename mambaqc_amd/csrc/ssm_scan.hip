@@ -25,15 +25,17 @@ int mqc_ssm_q_fwd(const void* q, const void* B, const void* S, const void* C, co
                   int64_t d_state, int dtype, void* stream) {
   if (batch < 0 || seq_len < 0 || d_inner < 0 || d_state < 0) return MQC_E_SHAPE;
   if (dtype != MQC_F32 && dtype != MQC_BF16 && dtype != MQC_F16) return MQC_E_DTYPE;
-  const bool work = batch > 0 && d_inner > 0 && (seq_len > 0 || h_last);
-  if (work && d_state == 0) return MQC_E_SHAPE;
-  if (work && (!q || !B || !S || !C || !D || !y)) return MQC_E_NULL;
+  // An empty walk (seq_len 0) still writes h_last: h0, or zeros without h0.
+  const bool steps = batch > 0 && d_inner > 0 && seq_len > 0;
+  const bool state_only = batch > 0 && d_inner > 0 && seq_len == 0 && h_last && d_state > 0;
+  if (steps && d_state == 0) return MQC_E_SHAPE;
+  if (steps && (!q || !B || !S || !C || !D || !y)) return MQC_E_NULL;
   if (batch > 65535 || d_inner > (1LL << 24) || d_state > 256) return MQC_E_LIMIT;
   SsmArgs a{};
   a.q = q; a.Sq = S; a.Dq = D; a.d_sb = d_sb; a.d_st = d_st; a.d_sd = d_sd;
   a.Bm = B; a.Cm = C; a.h0 = h0; a.y = y; a.h_last = h_last;
   a.batch = batch; a.T = seq_len; a.Dm = d_inner; a.S = d_state; a.eps = 0.f;
-  if (!work || seq_len == 0) return MQC_OK;
+  if (!steps && !state_only) return MQC_OK;
   return dispatch_ssm<MODE_Q>(a, dtype, (hipStream_t)stream);
 }
 
@@ -43,16 +45,18 @@ int mqc_ssm_fused_fwd(const void* delta, const void* s, const void* B, const voi
                       int64_t d_inner, int64_t d_state, float eps, int dtype, void* stream) {
   if (batch < 0 || seq_len < 0 || d_inner < 0 || d_state < 0) return MQC_E_SHAPE;
   if (dtype != MQC_F32 && dtype != MQC_BF16 && dtype != MQC_F16) return MQC_E_DTYPE;
-  const bool work = batch > 0 && d_inner > 0 && seq_len > 0;
-  if (work && d_state == 0) return MQC_E_SHAPE;
-  if (work && (!delta || !s || !B || !C || !lambda_alpha || !lambda_imag || !D || !y))
-    return MQC_E_NULL;
+  // An empty walk (seq_len 0) still writes h_last: h0, or zeros without h0.
+  const bool steps = batch > 0 && d_inner > 0 && seq_len > 0;
+  const bool state_only = batch > 0 && d_inner > 0 && seq_len == 0 && h_last && d_state > 0;
+  if (steps && d_state == 0) return MQC_E_SHAPE;
+  if (steps && (!delta || !s || !B || !C || !y)) return MQC_E_NULL;
+  if ((steps || state_only) && (!lambda_alpha || !lambda_imag || !D)) return MQC_E_NULL;
   if (batch > 65535 || d_inner > (1LL << 24) || d_state > 256) return MQC_E_LIMIT;
   SsmArgs a{};
   a.delta = delta; a.s = s; a.lam_alpha = lambda_alpha; a.lam_imag = lambda_imag; a.dvec = D;
   a.Bm = B; a.Cm = C; a.h0 = h0; a.y = y; a.h_last = h_last;
   a.batch = batch; a.T = seq_len; a.Dm = d_inner; a.S = d_state; a.eps = eps;
-  if (!work) return MQC_OK;
+  if (!steps && !state_only) return MQC_OK;
   return dispatch_ssm<MODE_DL>(a, dtype, (hipStream_t)stream);
 }
 

@@ -586,7 +586,9 @@ int launch_ssm_kpl(const SsmArgs& a, hipStream_t s) {
 // clamped onto the last KPL states).
 template <typename T, int MODE>
 int launch_ssm(const SsmArgs& a, hipStream_t s) {
-  if (a.batch == 0 || a.T == 0 || a.Dm == 0) return MQC_OK;
+  // T == 0 with h_last still launches: the walk is empty and the kernel writes
+  // h_last from h0 (or zeros).
+  if (a.batch == 0 || a.Dm == 0 || (a.T == 0 && !a.h_last)) return MQC_OK;
   // Per-(b, t) slices (and the strided D vector) are addressed with 32-bit lane
   // offsets; step counters are 32-bit.
   if (a.Dm * a.S * 4 * (int64_t)sizeof(T) >= ((int64_t)1 << 31)) return MQC_E_LIMIT;

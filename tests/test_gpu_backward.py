@@ -302,3 +302,28 @@ def test_causal_conv_silu_backward(shape, dtype):
     assert_close(xzg.grad, xzr.grad, tol(dtype), f"dx {shape} {dtype}")
     assert_close(wg.grad, wr.grad, tol(dtype), f"dw {shape} {dtype}")
     assert_close(bg.grad, br.grad, tol(dtype), f"dbias {shape} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_ssm_empty_sequence(dtype):
+    """seq_len 0: y is empty, the final state is h0 (zeros without h0), and the
+    backward passes dL/dh_last straight to h0 with zero parameter gradients."""
+    b, d, k = 2, 5, 16
+    ins = _dl_inputs(b, 0, d, k, seed=1, dtype=dtype)
+    g = torch.Generator().manual_seed(2)
+    h0 = torch.randn(b, d, k, 4, generator=g).to(dtype)
+    gh = torch.randn(b, d, k, 4, generator=g).to(dtype)
+
+    y, hl = K.ssm_forward_fused_dl(*(t.to(DEV) for t in ins), h0=h0.to(DEV), return_state=True)
+    assert y.shape == (b, 0, d, 4)
+    assert torch.equal(hl.cpu(), h0)
+    _, hl0 = K.ssm_forward_fused_dl(*(t.to(DEV) for t in ins), return_state=True)
+    assert (hl0 == 0).all()
+
+    got = [_leaf(t, DEV) for t in ins] + [_leaf(h0, DEV)]
+    y, hl = K.ssm_forward_fused_dl(*got[:7], h0=got[7], return_state=True)
+    (hl.float() * gh.to(DEV).float()).sum().backward()
+    assert torch.equal(hl.detach().cpu(), h0)
+    assert torch.equal(got[7].grad.cpu(), gh)
+    for t, name in zip(got[4:7], ["lambda_alpha", "lambda_imag", "D"]):
+        assert t.grad is not None and (t.grad == 0).all(), name

@@ -195,6 +195,24 @@ def test_ssm_forward_fused_wide(dtype):
     assert_close(got, want, tol(dtype), f"ssm_q wide {dtype}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_ssm_q_empty_walk_writes_state(dtype):
+    """mqc_ssm_q_fwd with seq_len 0 and an h_last buffer: h_last = h0, or zeros
+    without h0; the per-step operands may be NULL."""
+    from mambaqc_amd import _native as nat
+    b, d, k = 3, 7, 8
+    h0 = rnd(b, d, k, 4, seed=50, dtype=dtype).to(DEV)
+    lib = nat.load()
+    st = nat.stream_of(h0)
+    for src in (h0, None):
+        hl = torch.full_like(h0, 7.0)
+        rc = lib.mqc_ssm_q_fwd(None, None, None, None, None, 0, 0, 1, nat.ptr(src), None,
+                               hl.data_ptr(), b, 0, d, k, nat.dtype_code(h0), st)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert torch.equal(hl, h0 if src is not None else torch.zeros_like(h0))
+
+
 def test_ssm_forward_fused_strided_D():
     b, T, d, k = 2, 9, 4, 8
     q, Bm, S, C, _ = _q_inputs(b, T, d, k, seed=21, dtype=torch.float32)

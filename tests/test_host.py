@@ -157,6 +157,22 @@ def test_step_counter_limits_without_gpu():
                                  1e-6, 1, None) == -5
 
 
+def test_empty_walk_validation_without_gpu():
+    """seq_len 0 is work when the final state (or, in the backward, the
+    parameter partials) must be written: the parameters are then required, the
+    per-step operands are not; without an h_last buffer it is a no-op."""
+    lib = nat.load()
+    assert lib.mqc_ssm_fused_fwd(None, None, None, None, None, None, None, None, None, None,
+                                 2, 0, 3, 8, 1e-6, 1, None) == 0
+    assert lib.mqc_ssm_fused_fwd(None, None, None, None, None, None, None, None, None, FAKE,
+                                 2, 0, 3, 8, 1e-6, 1, None) == -1
+    assert lib.mqc_ssm_fused_fwd_train(None, None, None, None, None, None, None, None, None,
+                                       FAKE, None, 8, 2, 0, 3, 8, 1e-6, 1, None) == -1
+    assert lib.mqc_ssm_fused_bwd(None, None, None, None, None, None, None, None, None, 8, None,
+                                 None, None, None, None, None, None, None, None, None,
+                                 2, 0, 3, 8, 1e-6, 1, None) == -1
+
+
 def test_block_seeded_init_matches_reference():
     info = json.loads((GOLDEN / "init_c1.json").read_text())
     torch.manual_seed(0)
