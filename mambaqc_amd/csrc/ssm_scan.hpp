@@ -486,9 +486,12 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   }
 }
 
-// Steps of operands in flight per lane.
+// Steps of operands in flight per lane (six for four 16-bit states per lane:
+// measured at config 3 against four and eight).
 template <typename T, int KPL>
-constexpr int ssm_prefetch() { return KPL * (int)sizeof(T) >= 8 ? 4 : 8; }
+constexpr int ssm_prefetch() {
+  return KPL * (int)sizeof(T) >= 8 ? (sizeof(T) == 2 && KPL == 4 ? 6 : 4) : 8;
+}
 
 template <typename T, int MODE, int KPL, int G, int PF = ssm_prefetch<T, KPL>(),
           int NT = kSsmThreads, int SYNC = 0>
@@ -531,8 +534,8 @@ inline int64_t busiest_cu_waves(const SsmArgs& a, int G, int NT) {
 // the operands of two.
 template <typename T, int MODE, int KPL>
 constexpr int ssm_max_threads() {
-  if constexpr (MODE == MODE_DL) return KPL <= 2 ? 1024 : (sizeof(T) == 2 ? 768 : 512);
-  if constexpr (sizeof(T) == 2) return KPL == 1 ? 1024 : 768;
+  if constexpr (MODE == MODE_DL) return KPL <= 2 ? 1024 : 512;
+  if constexpr (sizeof(T) == 2) return KPL == 1 ? 1024 : (KPL == 2 ? 768 : 512);
   return KPL <= 2 ? 768 : 256;
 }
 
@@ -542,10 +545,12 @@ int launch_ssm_shape(const SsmArgs& a, hipStream_t s) {
   constexpr int kMaxNT = ssm_max_threads<T, MODE, KPL>();
   int best = 256;
   if constexpr (G <= 64) {
-    const int order[4] = {768, 1024, 512, 256};
+    // 384 threads (6 waves) only for four states per lane, where it puts one
+    // block on every CU at config 3.
+    const int order[5] = {768, 1024, 512, 384, 256};
     int64_t best_w = -1;
     for (int nt : order) {
-      if (nt % G != 0 || nt > kMaxNT) continue;
+      if (nt % G != 0 || nt > kMaxNT || (nt == 384 && KPL != 4)) continue;
       const int64_t w = busiest_cu_waves(a, G, nt);
       if (best_w < 0 || w < best_w) {
         best_w = w;
@@ -562,6 +567,9 @@ int launch_ssm_shape(const SsmArgs& a, hipStream_t s) {
       break;
     case 512:
       if constexpr (kMaxNT >= 512) return launch_ssm_g<T, MODE, KPL, G, PF, 512, 1>(a, s);
+      break;
+    case 384:
+      if constexpr (KPL == 4 && kMaxNT >= 384) return launch_ssm_g<T, MODE, KPL, G, PF, 384, 1>(a, s);
       break;
     default:
       break;
@@ -616,6 +624,17 @@ int launch_ssm(const SsmArgs& a, hipStream_t s) {
     // T 2048, D 1536, S 64: batch 1 1.063 -> 1.001 ms, batch 2 1.391 -> 1.340 ms.
     const int64_t waves_kpl2 = a.batch * a.Dm * ((a.S + 1) / 2) / 64;
     if (a.S <= 64 && waves_kpl2 < 12 * kCUs) return launch_ssm_kpl<T, MODE, 1>(a, s);
+    // Four states per lane (32 bytes of B and C per lane and step, 384-thread
+    // blocks, six steps in flight) for the inference walk: fewer k-sum and
+    // per-step instructions per state and half the waves at each barrier.
+    // Measured at T 2048, S 64 (bf16), same buffers, against two states per
+    // lane: B4 d_inner 1536 2.288 -> 2.221 ms, B8 d1536 4.765 -> 4.724,
+    // B4 d2048 3.126 -> 3.088, B4 d3072 4.381 -> 4.319, B16 d768 4.383 -> 4.334,
+    // B2 d3072 2.299 -> 2.229; B6 d1536 4.074 -> 4.131. The training walk
+    // (checkpoints) measured 36 % slower with four states and keeps two.
+    if constexpr (MODE == MODE_DL) {
+      if (a.S <= 64 && !a.h_ckpt && wide_ok(4)) return launch_ssm_kpl<T, MODE, 4>(a, s);
+    }
     if (a.S <= 128 && wide_ok(2)) return launch_ssm_kpl<T, MODE, 2>(a, s);
     if (a.S <= 64) return launch_ssm_kpl<T, MODE, 1>(a, s);
     if (a.S <= 256 && wide_ok(4)) return launch_ssm_kpl<T, MODE, 4>(a, s);

@@ -255,12 +255,14 @@ def _dl_inputs(b, T, d, k, seed, dtype):
                                    # (3 x 13 = 39) multiples of the 8 XCDs: the remapped and the
                                    # hardware block order
                                    (2, 37, 64, 64), (4, 19, 96, 64), (3, 21, 100, 64),
-                                   # enough (b, d) for two states per lane in 16-bit storage
-                                   # (>= 12 waves per CU) and 768-thread blocks; d ragged;
+                                   # enough (b, d) for several states per lane in 16-bit storage
+                                   # (two, or four for the inference walk); d ragged;
                                    # walks shorter than, equal to and past one group of 8
                                    # prefetched steps (a tail of 5)
                                    (8, 5, 768, 64), (3, 7, 2050, 64), (8, 8, 768, 64),
-                                   (8, 21, 768, 64)])
+                                   (8, 21, 768, 64),
+                                   # four states per lane with lanes past d_state (48 of 64)
+                                   (8, 9, 1024, 48)])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_ssm_fused_dl(shape, dtype):
     a = _dl_inputs(*shape, seed=sum(shape), dtype=dtype)
