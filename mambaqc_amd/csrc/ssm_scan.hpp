@@ -441,9 +441,10 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   // Lanes that load 8 bytes of B and C per step (one 16-bit state) keep the
   // ring in flight across groups: measured at T 2048, D 1536, S 64 (bf16),
   // batch 1 1.00 -> 0.89 ms and batch 2 1.34 -> 1.25 ms. Lanes that load 16
-  // bytes still wait for all their loads once per group, which measured
-  // 0.5-1.5 % faster at the config-3 shape (B4 T2048 D1536 S64) than keeping
-  // PF steps in flight, and the same with 4 or 6 steps.
+  // bytes or more still wait for all their loads once per group, which
+  // measured 0.5-1.5 % faster at the config-3 shape (B4 T2048 D1536 S64) than
+  // keeping PF steps in flight, the same with 4 or 6 steps, and 0-2 % faster
+  // for four states per lane (32 bytes) with 4 or 8 steps.
   constexpr bool DRAIN = KPL * 4 * sizeof(T) >= 16;
   // s_waitcnt vmcnt(0) with expcnt and lgkmcnt at their maxima (gfx9 fields:
   // vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in bits [15:14]).
