@@ -546,12 +546,13 @@ int launch_ssm_shape(const SsmArgs& a, hipStream_t s) {
   constexpr int kMaxNT = ssm_max_threads<T, MODE, KPL>();
   int best = 256;
   if constexpr (G <= 64) {
-    // 384 threads (6 waves) only for four states per lane, where it puts one
-    // block on every CU at config 3.
+    // 384 threads (6 waves) only for lanes with 32 bytes of each operand per
+    // step (four 16-bit or two fp32 states), where it puts one block on every
+    // CU at config 3.
     const int order[5] = {768, 1024, 512, 384, 256};
     int64_t best_w = -1;
     for (int nt : order) {
-      if (nt % G != 0 || nt > kMaxNT || (nt == 384 && KPL != 4)) continue;
+      if (nt % G != 0 || nt > kMaxNT || (nt == 384 && KPL * sizeof(T) != 8)) continue;
       const int64_t w = busiest_cu_waves(a, G, nt);
       if (best_w < 0 || w < best_w) {
         best_w = w;
@@ -570,7 +571,7 @@ int launch_ssm_shape(const SsmArgs& a, hipStream_t s) {
       if constexpr (kMaxNT >= 512) return launch_ssm_g<T, MODE, KPL, G, PF, 512, 1>(a, s);
       break;
     case 384:
-      if constexpr (KPL == 4 && kMaxNT >= 384) return launch_ssm_g<T, MODE, KPL, G, PF, 384, 1>(a, s);
+      if constexpr (KPL * sizeof(T) == 8 && kMaxNT >= 384) return launch_ssm_g<T, MODE, KPL, G, PF, 384, 1>(a, s);
       break;
     default:
       break;
@@ -641,6 +642,14 @@ int launch_ssm(const SsmArgs& a, hipStream_t s) {
     if (a.S <= 256 && wide_ok(4)) return launch_ssm_kpl<T, MODE, 4>(a, s);
     return MQC_E_LIMIT;
   } else {
+    // fp32: two states per lane (32 bytes of each operand per lane and step)
+    // once that still gives 6 waves per CU, except in the training walk.
+    // Measured at S 64, same buffers, against one state per lane: delta-lambda
+    // form B4 T2048 d1536 4.66 -> 4.45 ms, B8 T1024 d1536 4.75 -> 4.57,
+    // B4 T1024 d3072 4.51 -> 4.37, B2 T2048 d1536 2.34 -> 2.33; q form
+    // B4 T1024 d1536 3.38 -> 3.26, B8 T512 d1536 3.46 -> 3.31.
+    if (a.S <= 64 && !a.h_ckpt && wide_ok(2) && a.batch * a.Dm * (a.S / 2) / 64 >= 6 * kCUs)
+      return launch_ssm_kpl<T, MODE, 2>(a, s);
     if (a.S <= 64) return launch_ssm_kpl<T, MODE, 1>(a, s);
     if (a.S <= 128 && wide_ok(2)) return launch_ssm_kpl<T, MODE, 2>(a, s);
     if (a.S <= 256 && wide_ok(4)) return launch_ssm_kpl<T, MODE, 4>(a, s);

@@ -313,9 +313,15 @@ def test_ssm_front_unaligned_views():
     assert torch.equal(d1, d2) and torch.equal(s1, s2)
 
 
-def test_ssm_fused_dl_state_carry():
-    """Running [0, T) equals running [0, t1) then [t1, T) from the carried state."""
-    a = _dl_inputs(2, 40, 6, 64, seed=41, dtype=torch.float32)
+@pytest.mark.parametrize("shape,dtype", [((2, 40, 6, 64), torch.float32),
+                                         # several states per lane (2 in fp32, 4 in bf16)
+                                         ((8, 20, 768, 64), torch.float32),
+                                         ((8, 20, 768, 64), torch.bfloat16)])
+def test_ssm_fused_dl_state_carry(shape, dtype):
+    """Running [0, T) equals running [0, t1) then [t1, T) from the carried state
+    (exactly in fp32, where the state is carried in fp32; to the 16-bit
+    tolerance in bf16, where h_last is stored in bf16)."""
+    a = _dl_inputs(*shape, seed=41, dtype=dtype)
     dev = [t.to(DEV) for t in a]
     delta, s, Bm, C, la, li, D = dev
     y_full, h_full = K.ssm_forward_fused_dl(*dev, return_state=True)
@@ -323,10 +329,12 @@ def test_ssm_fused_dl_state_carry():
                                     return_state=True)
     y2, h2 = K.ssm_forward_fused_dl(delta[:, 15:], s[:, 15:], Bm[:, 15:], C[:, 15:], la, li, D,
                                     h0=h1, return_state=True)
-    assert_close(torch.cat([y1, y2], 1), y_full, 1e-5, "carry y")
-    assert_close(h2, h_full, 1e-5, "carry h")
+    t_carry = 1e-5 if dtype == torch.float32 else tol(dtype)
+    assert_close(torch.cat([y1, y2], 1), y_full, t_carry, "carry y")
+    assert_close(h2, h_full, t_carry, "carry h")
     ref_y, ref_h = oracle.ssm_forward_dl_reference(*(up(t) for t in a), return_state=True)
-    assert_close(h_full, ref_h, 1e-4, "final state vs oracle")
+    assert_close(y_full, ref_y, tol(dtype), "y vs oracle")
+    assert_close(h_full, ref_h, tol(dtype), "final state vs oracle")
 
 
 def test_ssm_fused_dl_config3_full_size():
