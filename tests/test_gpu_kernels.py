@@ -261,8 +261,9 @@ def _dl_inputs(b, T, d, k, seed, dtype):
                                    # prefetched steps (a tail of 5)
                                    (8, 5, 768, 64), (3, 7, 2050, 64), (8, 8, 768, 64),
                                    (8, 21, 768, 64),
-                                   # four states per lane with lanes past d_state (48 of 64)
-                                   (8, 9, 1024, 48)])
+                                   # four states per lane with lanes past d_state (48 of 64),
+                                   # and with a 4-lane group (d_state 16)
+                                   (8, 9, 1024, 48), (16, 5, 1536, 16)])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_ssm_fused_dl(shape, dtype):
     a = _dl_inputs(*shape, seed=sum(shape), dtype=dtype)
