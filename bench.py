@@ -106,13 +106,14 @@ def ssm_inputs(blk, x):
     return delta, s, Bq, Cq
 
 
-def cpu_baseline(blk, x, t_sample=128):
+def cpu_baseline(blk, x, t_sample=256):
     """Oracle block forward (fp32, CPU) on the first t_sample steps of the same
-    input, with the same weights. The sequential path's cost is linear in T."""
+    input, with the same weights, on every core this process may run on. The
+    sequential path's cost is linear in T."""
     import torch
     import oracle
 
-    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16")))
+    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     sd = {k: v.detach().float().cpu() for k, v in blk.state_dict().items()}
     xs = x[:, :t_sample].float().cpu()

@@ -40,11 +40,12 @@ extern "C" {
                               * SSM entry points: seq_len >= 2^30, d_state above the
                               * stated maximum, one (b, t) slice of B/C of 2 GiB or
                               * more, or a negative or too large D stride) */
+#define MQC_E_SPACE (-6)     /* a workspace is smaller than the call needs */
 
 /* Human-readable text for a status code (static storage, never NULL). */
 const char* mqc_status_string(int status);
 
-/* ABI version: bumped whenever a signature changes. */
+/* ABI version: bumped whenever a signature or an argument's meaning changes. */
 int mqc_abi_version(void);
 
 /* out = p (x) q, Hamilton product of n_quat quaternions. p, q, out: dtype.
@@ -102,10 +103,12 @@ int mqc_ssm_q_fwd(const void* q, const void* B, const void* S, const void* C, co
  *   y_t = sum_k C_{t,k} (x) h_{t,k} + (D[d] * s[b,t,d], 0, 0, 0)
  * delta, s: dtype [batch, seq_len, d_inner]; B, C: dtype
  * [batch, seq_len, d_inner, d_state, 4]; lambda_alpha: fp32 [d_inner, d_state];
- * lambda_imag: fp32 [d_inner, d_state, 3]; D: fp32 [d_inner]; h0: dtype
+ * lambda_imag: fp32 [d_inner, d_state, 3]; D: fp32 [d_inner]; h0: fp32
  * [batch, d_inner, d_state, 4] or NULL; y: dtype [batch, seq_len, d_inner, 4];
- * h_last: dtype [batch, d_inner, d_state, 4] or NULL. With seq_len 0, h_last (if
- * given) receives h0, or zeros; delta, s, B, C and y may then be NULL, the
+ * h_last: fp32 [batch, d_inner, d_state, 4] or NULL. The state is carried in
+ * fp32 whatever dtype is, so a walk split into pieces (recurrent decoding)
+ * gives the same y as the whole walk. With seq_len 0, h_last (if given)
+ * receives h0, or zeros; delta, s, B, C and y may then be NULL, the
  * parameters may not.
  * Replaces the body of QuaternionMamba2Block._ssm_forward,
  * mambaqc/models/quaternion_mamba2_block.py:206-228 (Lambda, z = delta*Lambda,
@@ -114,6 +117,40 @@ int mqc_ssm_fused_fwd(const void* delta, const void* s, const void* B, const voi
                       const float* lambda_alpha, const float* lambda_imag, const float* D,
                       const void* h0, void* y, void* h_last, int64_t batch, int64_t seq_len,
                       int64_t d_inner, int64_t d_state, float eps, int dtype, void* stream);
+
+/* Chunk length mqc_ssm_fused_fwd_chunked would be given by a caller that lets
+ * the library choose: seq_len (one chunk, the whole walk) when batch * d_inner
+ * * d_state states keep the GPU busy on their own, shorter chunks (at least 64
+ * steps, at most 8 chunks) when they do not. Negative: an MQC_E_* code. */
+int64_t mqc_ssm_chunk_len_auto(int64_t batch, int64_t seq_len, int64_t d_inner,
+                               int64_t d_state, int dtype);
+
+/* Bytes of workspace mqc_ssm_fused_fwd_chunked needs for these sizes:
+ * 24 * batch * (n_chunks - 1) * d_inner * d_state with n_chunks =
+ * ceil(seq_len / chunk_len) (0 for one chunk). Negative: an MQC_E_* code. */
+int64_t mqc_ssm_chunked_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_inner,
+                                        int64_t d_state, int64_t chunk_len);
+
+/* mqc_ssm_fused_fwd with the seq axis cut into chunks of chunk_len steps that
+ * are walked side by side (the last chunk may be shorter): each chunk but the
+ * last is first reduced to its transition (P = product of its q's, H = its end
+ * state from zero), an associative scan over the chunks (the later transition
+ * on the left) gives every chunk its start state, then every chunk is walked
+ * from it. Same arguments and results as mqc_ssm_fused_fwd (h0, h_last fp32),
+ * up to rounding; for batches too small to fill the GPU through
+ * batch * d_inner * d_state alone. workspace: device memory of at least
+ * mqc_ssm_chunked_workspace_bytes (16-byte aligned; may be NULL when
+ * chunk_len >= seq_len), owned by the caller, no contents needed on entry.
+ * d_state <= 64 when there is more than one chunk; batch * n_chunks <= 65535.
+ * Replaces, like mqc_ssm_fused_fwd, mambaqc/models/quaternion_mamba2_block.py:206-228
+ * (the sequential walk of kernels/ssm_fused.py:363-379); the chunked order of
+ * evaluation follows the associative-scan idea of kernels/parallel_scan.py:171-264. */
+int mqc_ssm_fused_fwd_chunked(const void* delta, const void* s, const void* B, const void* C,
+                              const float* lambda_alpha, const float* lambda_imag, const float* D,
+                              const void* h0, void* y, void* h_last, int64_t batch,
+                              int64_t seq_len, int64_t d_inner, int64_t d_state,
+                              int64_t chunk_len, float eps, int dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream);
 
 /* Quaternion LayerNorm over the d axis of each of `rows` rows of d quaternions:
  *   n = sqrt(|q|^2 + eps); mu, var = mean and biased variance of n over d;
@@ -167,7 +204,7 @@ int mqc_causal_conv_silu_bwd(const void* x, int64_t x_row_stride, const float* w
  * backward keeps K steps of operands and states in registers). */
 int mqc_ssm_bwd_ckpt_every(int dtype);
 
-/* mqc_ssm_fused_fwd plus fp32 state checkpoints for the backward:
+/* mqc_ssm_fused_fwd (h0, h_last fp32) plus fp32 state checkpoints for the backward:
  * h_ckpt [batch, ceil(seq_len / ckpt_every), d_inner, d_state, 4] receives the
  * state at the last step of every chunk of ckpt_every steps (the last chunk may
  * be shorter). With seq_len 0 it has no entries and may be NULL. */
@@ -178,14 +215,14 @@ int mqc_ssm_fused_fwd_train(const void* delta, const void* s, const void* B, con
                             int64_t d_state, float eps, int dtype, void* stream);
 
 /* Backward of mqc_ssm_fused_fwd_train given gy = dL/dy (dtype [batch, seq_len,
- * d_inner, 4]) and optionally dh_last = dL/dh_last (dtype [batch, d_inner,
+ * d_inner, 4]) and optionally dh_last = dL/dh_last (fp32 [batch, d_inner,
  * d_state, 4]). Writes d_delta, d_s (fp32 [batch, seq_len, d_inner]: these
  * sums over d_state keep fp32 precision for callers whose delta is fp32, as
  * under autocast), dB, dC (dtype, shape of B), per-batch partial parameter gradients
  * dlambda_alpha_part fp32 [batch, d_inner, d_state],
  * dlambda_imag_part fp32 [batch, d_inner, d_state, 3], dD_part fp32
- * [batch, d_inner] (the caller sums them over batch), and dh0 (dtype
- * [batch, d_inner, d_state, 4]) if non-NULL. h0 and h_ckpt must be the forward's;
+ * [batch, d_inner] (the caller sums them over batch), and dh0 (fp32
+ * [batch, d_inner, d_state, 4]) if non-NULL. h0 (fp32) and h_ckpt must be the forward's;
  * ckpt_every must equal mqc_ssm_bwd_ckpt_every(dtype); d_state <= 64. With
  * seq_len 0 the partials are zeros and dh0 = dh_last (zeros without it); the
  * per-step tensors and h_ckpt may then be NULL. */

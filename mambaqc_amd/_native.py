@@ -55,9 +55,18 @@ SIGNATURES = {
     "mqc_conv_run_length": [],
     "mqc_causal_conv_silu_bwd": [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64,
                                  _i64, _i64, _int, _vp],
+    "mqc_ssm_fused_fwd_chunked": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                  _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp, _i64, _vp],
 }
 
-ABI_VERSION = 3
+# name -> argtypes of the entry points that return int64_t (a size, or a
+# negative status code)
+SIGNATURES_I64 = {
+    "mqc_ssm_chunk_len_auto": [_i64, _i64, _i64, _i64, _int],
+    "mqc_ssm_chunked_workspace_bytes": [_i64, _i64, _i64, _i64, _i64],
+}
+
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib = None
@@ -85,6 +94,10 @@ def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = argtypes
             fn.restype = _int
+        for name, argtypes in SIGNATURES_I64.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = _i64
         lib.mqc_status_string.argtypes = [_int]
         lib.mqc_status_string.restype = ctypes.c_char_p
         lib.mqc_abi_version.argtypes = []

@@ -156,7 +156,8 @@ class QuaternionMamba2Block(nn.Module):
 
         state = (conv_tail, h): conv_tail [batch, d_conv - 1, d_inner] holds the
         last d_conv - 1 conv inputs, h [batch, d_inner, d_state, 4] the SSM
-        state. None starts from zeros, where the result equals forward(x).
+        state, in fp32 whatever the model dtype (the precision the walk
+        carries it in). None starts from zeros, where the result equals forward(x).
         Feeding a sequence in pieces gives the same outputs as feeding it whole
         (up to rounding), which is what recurrent decoding relies on.
         """

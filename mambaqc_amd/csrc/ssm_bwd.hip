@@ -67,10 +67,10 @@ int mqc_ssm_fused_bwd(const void* delta, const void* s, const void* B, const voi
   if (ckpt_every != mqc_ssm_bwd_ckpt_every(dtype)) return MQC_E_LIMIT;
   SsmBwdArgs a{};
   a.delta = delta; a.s = s; a.Bm = B; a.Cm = C; a.lam_alpha = lambda_alpha;
-  a.lam_imag = lambda_imag; a.dvec = D; a.h0 = h0; a.h_ckpt = h_ckpt; a.gy = gy;
-  a.dh_last = dh_last; a.d_delta = d_delta; a.d_s = d_s; a.dB = dB; a.dC = dC;
+  a.lam_imag = lambda_imag; a.dvec = D; a.h0 = (const float*)h0; a.h_ckpt = h_ckpt; a.gy = gy;
+  a.dh_last = (const float*)dh_last; a.d_delta = d_delta; a.d_s = d_s; a.dB = dB; a.dC = dC;
   a.dalpha_part = dlambda_alpha_part; a.dimag_part = dlambda_imag_part; a.dD_part = dD_part;
-  a.dh0 = dh0; a.batch = batch; a.T = seq_len; a.Dm = d_inner; a.S = d_state; a.eps = eps;
+  a.dh0 = (float*)dh0; a.batch = batch; a.T = seq_len; a.Dm = d_inner; a.S = d_state; a.eps = eps;
   if (!steps && !empty_walk) return MQC_OK;
   switch (dtype) {
     case MQC_F32: return launch_ssm_bwd<float>(a, (hipStream_t)stream);

@@ -53,10 +53,10 @@ struct SsmBwdArgs {
   const float* lam_alpha;  // [D,S]
   const float* lam_imag;   // [D,S,3]
   const float* dvec;       // [D]
-  const void* h0;          // [B,D,S,4] dtype or null
+  const float* h0;         // [B,D,S,4] fp32 or null
   const float* h_ckpt;     // [B,nC,D,S,4] fp32
   const void* gy;          // [B,T,D,4] dtype
-  const void* dh_last;     // [B,D,S,4] dtype or null
+  const float* dh_last;    // [B,D,S,4] fp32 or null
   float* d_delta;          // [B,T,D] fp32
   float* d_s;              // [B,T,D] fp32
   void* dB;                // [B,T,D,S,4] dtype
@@ -64,7 +64,7 @@ struct SsmBwdArgs {
   float* dalpha_part;      // [B,D,S]
   float* dimag_part;       // [B,D,S,3]
   float* dD_part;          // [B,D]
-  void* dh0;               // [B,D,S,4] dtype or null
+  float* dh0;              // [B,D,S,4] fp32 or null
   int64_t batch, T, Dm, S;
   float eps;
 };
@@ -191,7 +191,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
   quat carry{0.f, 0.f, 0.f, 0.f};
   if (a.dh_last) {
     float e[4];
-    load_vec<T, 4>((const T*)a.dh_last + sidx, e);
+    load_vec<float, 4>(a.dh_last + sidx, e);
     carry = quat_from(e);
   }
 
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
       hs[0] = quat{o.h_in.x, o.h_in.y, o.h_in.z, o.h_in.w};
     } else if (a.h0) {
       float e[4];
-      load_vec<T, 4>((const T*)a.h0 + sidx, e);
+      load_vec<float, 4>(a.h0 + sidx, e);
       hs[0] = quat_from(e);
     } else {
       hs[0] = quat{0.f, 0.f, 0.f, 0.f};
@@ -346,7 +346,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
   if (own) {
     if (a.dh0) {
       const float e[4] = {carry.w, carry.x, carry.y, carry.z};
-      store_vec<T, 4>((T*)a.dh0 + sidx, e);
+      store_vec<float, 4>(a.dh0 + sidx, e);
     }
     float da, dv[3];
     pull_finish(pacc, L, da, dv);
@@ -393,8 +393,8 @@ int launch_ssm_bwd(const SsmBwdArgs& a, hipStream_t s) {
   if (a.T >= ((int64_t)1 << 30)) return MQC_E_LIMIT;
   const uintptr_t qa = 4 * sizeof(T);
   if (!aligned(a.Bm, qa) || !aligned(a.Cm, qa) || !aligned(a.gy, qa) || !aligned(a.dB, qa) ||
-      !aligned(a.dC, qa) || !aligned(a.h_ckpt, 16) || (a.h0 && !aligned(a.h0, qa)) ||
-      (a.dh_last && !aligned(a.dh_last, qa)) || (a.dh0 && !aligned(a.dh0, qa)) ||
+      !aligned(a.dC, qa) || !aligned(a.h_ckpt, 16) || (a.h0 && !aligned(a.h0, 16)) ||
+      (a.dh_last && !aligned(a.dh_last, 16)) || (a.dh0 && !aligned(a.dh0, 16)) ||
       !aligned(a.delta, sizeof(T)) || !aligned(a.s, sizeof(T)) || !aligned(a.d_delta, 4) ||
       !aligned(a.d_s, 4))
     return MQC_E_ALIGN;

@@ -1,0 +1,6 @@
+// Instantiation of the time-chunked fused SSM walk for f16 storage (ssm_chunk.hpp).
+#include "ssm_chunk.hpp"
+
+namespace mqc {
+template int ssm_chunk_launch<f16_t>(const SsmArgs&, float*, hipStream_t);
+}  // namespace mqc

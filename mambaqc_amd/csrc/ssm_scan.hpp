@@ -169,6 +169,14 @@ struct SsmArgs {
   int64_t ckpt_every;
   int64_t batch, T, Dm, S;
   float eps;
+  // Chunked walk (MODE_DL inference, ssm_chunk.hpp): the T axis in n_chunks
+  // chunks of chunk_len steps (the last may be shorter), one row of blocks per
+  // (chunk, batch); chunk c > 0 starts from the state at the end of chunk c-1,
+  // h_chunk[b, c-1] (fp32 [B, n_chunks - 1, D, S, 4]). n_chunks 1 (chunk_len
+  // 0 or T) is the whole walk from h0.
+  int64_t chunk_len = 0;
+  int64_t n_chunks = 1;
+  const float* h_chunk = nullptr;
 };
 
 template <typename T, int MODE, int KPL>
@@ -259,12 +267,18 @@ __device__ inline LamConst lam_const(const float* lam_alpha, const float* lam_im
 // q = Cayley(dl * Lambda) = ((1 - dl^2 n2) / N, dl v / N), N = max(1 - dl a + dl^2 n2, eps).
 // The forward kernel and the backward's recompute share this code, so both
 // produce the same q.
-__device__ inline quat cayley_step(float dl, float dl2, const LamConst& L, float eps) {
+// c receives dl / max(N, eps), the factor on v: q = q.w + c v.
+__device__ inline quat cayley_step_c(float dl, float dl2, const LamConst& L, float eps, float& c) {
   float N = fmaf(dl2, L.n2, fmaf(-dl, L.a, 1.f));
   N = fmaxf(N, eps);
   const float r = __builtin_amdgcn_rcpf(N);
-  const float c = dl * r;
+  c = dl * r;
   return quat{fmaf(-dl2, L.n2, 1.f) * r, c * L.v0, c * L.v1, c * L.v2};
+}
+
+__device__ inline quat cayley_step(float dl, float dl2, const LamConst& L, float eps) {
+  float c;
+  return cayley_step_c(dl, dl2, L, eps, c);
 }
 
 // h_t = q (x) h_{t-1} + s * B
@@ -285,8 +299,11 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int j = tid & (G - 1);
-  int64_t bx, b;
-  xcd_block(bx, b);
+  int64_t bx, by;
+  xcd_block(bx, by);
+  // Block row by = chunk * batch + b (one chunk, the whole walk, unless chunked).
+  const int chunk = a.n_chunks > 1 ? (int)(by / a.batch) : 0;
+  const int64_t b = a.n_chunks > 1 ? by - (int64_t)chunk * a.batch : by;
   const int64_t d_raw = bx * GPB + tid / G;
   const bool gvalid = d_raw < a.Dm;
   const int64_t d = gvalid ? d_raw : a.Dm - 1;
@@ -297,6 +314,10 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   // Step counters are 32-bit (the host checks T): gfx9's scalar unit has no
   // 64-bit compares, and 64-bit ones would run on the VALU every step.
   const int Tn = (int)a.T;
+  // This block's steps: [tb, tb + Tw).
+  const int Lc = a.n_chunks > 1 ? (int)a.chunk_len : Tn;
+  const int tb = chunk * Lc;
+  const int Tw = Tn - tb < Lc ? Tn - tb : Lc;
   const int64_t rowBC = a.Dm * a.S * 4;  // elements per (b, t) slice of B, C, q
   const int64_t rowTok = a.Dm;           // elements per (b, t) slice of delta, s
   // Byte offsets of this lane inside one (b, t) slice (the host checks that a
@@ -315,13 +336,24 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
     dskip = a.dvec[d];
   }
 
-  // States.
+  // States. The block's form (MODE_DL) takes and returns the state in fp32,
+  // the precision it is carried in here, so a walk split into pieces (the
+  // recurrent decode) equals the whole walk; the q form keeps the reference's
+  // convention of a state in the operands' dtype (ssm_fused.py:297-298).
+  using HT = typename std::conditional<MODE == MODE_DL, float, T>::type;
   quat h[KPL];
 #pragma unroll
   for (int kk = 0; kk < KPL; ++kk) h[kk] = quat{0.f, 0.f, 0.f, 0.f};
-  if (a.h0) {
+  if (chunk > 0) {
+    // The state at the end of the previous chunk (fp32, from the carry prefix).
     float e[4 * KPL];
-    load_vec<T, 4 * KPL>((const T*)a.h0 + ((b * a.Dm + d) * a.S + k0) * 4, e);
+    load_vec<float, 4 * KPL>(
+        a.h_chunk + (((b * (a.n_chunks - 1) + chunk - 1) * a.Dm + d) * a.S + k0) * 4, e);
+#pragma unroll
+    for (int kk = 0; kk < KPL; ++kk) h[kk] = quat_from(&e[4 * kk]);
+  } else if (a.h0) {
+    float e[4 * KPL];
+    load_vec<HT, 4 * KPL>((const HT*)a.h0 + ((b * a.Dm + d) * a.S + k0) * 4, e);
 #pragma unroll
     for (int kk = 0; kk < KPL; ++kk) h[kk] = quat_from(&e[4 * kk]);
   }
@@ -344,7 +376,7 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   };
 
   Step<T, MODE, KPL> ring[PF];
-  const int t_last = Tn - 1;
+  const int t_last = tb + Tw - 1;
 
   const bool writer = gvalid && (G < 4 || j < 4);
   const int64_t rowY = a.Dm * 4;
@@ -389,7 +421,7 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
     // re-reads the last step, which keeps the loads unconditional).
     if constexpr (REFILL) {
       const int tn = t + PF;
-      load_step(cur, tn < Tn ? tn : t_last);
+      load_step(cur, tn <= t_last ? tn : t_last);
     }
     if constexpr (!FULL) {
       if (!kvalid) acc = quat{0.f, 0.f, 0.f, 0.f};
@@ -449,41 +481,42 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   // s_waitcnt vmcnt(0) with expcnt and lgkmcnt at their maxima (gfx9 fields:
   // vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in bits [15:14]).
   constexpr int kWaitVm0 = 0x0F70;
+  // Step counters below are relative to tb.
   int t0 = 0;
-  if (Tn >= PF) {
+  if (Tw >= PF) {
     // The scheduling barriers keep the prologue's loads in slot order.
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      load_step(ring[i], i);
+      load_step(ring[i], tb + i);
       __builtin_amdgcn_sched_barrier(0);
     }
-    for (; t0 + PF <= Tn; t0 += PF) {
+    for (; t0 + PF <= Tw; t0 += PF) {
       if constexpr (DRAIN) __builtin_amdgcn_s_waitcnt(kWaitVm0);
 #pragma unroll
-      for (int i = 0; i < PF; ++i) walk_step(std::true_type{}, ring[i], t0 + i);
+      for (int i = 0; i < PF; ++i) walk_step(std::true_type{}, ring[i], tb + t0 + i);
       if constexpr (SYNC == 2) __syncthreads();
     }
   } else {
     // A walk shorter than PF (a decode step has T = 1) loads only its steps.
 #pragma unroll
     for (int i = 0; i < PF; ++i)
-      if (i < Tn) load_step(ring[i], i);
+      if (i < Tw) load_step(ring[i], tb + i);
   }
-  if (t0 < Tn) {
+  if (t0 < Tw) {
 #pragma unroll
     for (int i = 0; i < PF; ++i)
-      if (t0 + i < Tn) walk_step(std::false_type{}, ring[i], t0 + i);
+      if (t0 + i < Tw) walk_step(std::false_type{}, ring[i], tb + t0 + i);
     if constexpr (SYNC == 2) __syncthreads();
   }
 
-  if (a.h_last && gvalid && kvalid) {
+  if (a.h_last && gvalid && kvalid && chunk == a.n_chunks - 1) {
     float e[4 * KPL];
 #pragma unroll
     for (int kk = 0; kk < KPL; ++kk) {
       e[4 * kk + 0] = h[kk].w; e[4 * kk + 1] = h[kk].x;
       e[4 * kk + 2] = h[kk].y; e[4 * kk + 3] = h[kk].z;
     }
-    store_vec<T, 4 * KPL>((T*)a.h_last + ((b * a.Dm + d) * a.S + k0) * 4, e);
+    store_vec<HT, 4 * KPL>((HT*)a.h_last + ((b * a.Dm + d) * a.S + k0) * 4, e);
   }
 }
 
@@ -499,8 +532,9 @@ template <typename T, int MODE, int KPL, int G, int PF = ssm_prefetch<T, KPL>(),
 int launch_ssm_g(const SsmArgs& a, hipStream_t s) {
   constexpr int GPB = NT / G;
   const int64_t gx = (a.Dm + GPB - 1) / GPB;
-  if (gx > 0x7fffffffLL || a.batch > 65535) return MQC_E_LIMIT;
-  const dim3 grid((unsigned)gx, (unsigned)a.batch);
+  const int64_t gy = a.batch * a.n_chunks;  // (chunk, batch) rows
+  if (gx > 0x7fffffffLL || gy > 65535) return MQC_E_LIMIT;
+  const dim3 grid((unsigned)gx, (unsigned)gy);
   if (a.S == (int64_t)KPL * G)
     ssm_scan_kernel<T, MODE, KPL, G, PF, NT, true, SYNC><<<grid, dim3(NT), 0, s>>>(a);
   else
@@ -524,7 +558,7 @@ constexpr int kCUs = 256;  // MI355X compute units
 
 inline int64_t busiest_cu_waves(const SsmArgs& a, int G, int NT) {
   const int64_t gpb = NT / G;
-  const int64_t blocks = a.batch * ((a.Dm + gpb - 1) / gpb);
+  const int64_t blocks = a.batch * a.n_chunks * ((a.Dm + gpb - 1) / gpb);
   return (blocks + kCUs - 1) / kCUs * (NT / 64);
 }
 
@@ -609,22 +643,25 @@ int launch_ssm(const SsmArgs& a, hipStream_t s) {
   if (MODE == MODE_Q && (a.d_sd < 0 || (a.Dm - 1) * a.d_sd * (int64_t)sizeof(T) >= ((int64_t)1 << 31)))
     return MQC_E_LIMIT;
   const uintptr_t qa = 4 * sizeof(T);
+  // The state (h0, h_last) is fp32 in MODE_DL, the operands' dtype in MODE_Q.
+  const uintptr_t ha = MODE == MODE_DL ? 16 : qa;
   if (!aligned(a.Bm, qa) || !aligned(a.Cm, qa) || !aligned(a.y, sizeof(T)) ||
       (MODE == MODE_Q && (!aligned(a.q, qa) || !aligned(a.Sq, qa) || !aligned(a.Dq, sizeof(T)))) ||
-      (a.h0 && !aligned(a.h0, qa)) || (a.h_last && !aligned(a.h_last, qa)))
+      (a.h0 && !aligned(a.h0, ha)) || (a.h_last && !aligned(a.h_last, ha)))
     return MQC_E_ALIGN;
   auto wide_ok = [&](int kpl) {
     const uintptr_t al = kpl * 4 * sizeof(T) >= 16 ? 16 : kpl * 4 * sizeof(T);
+    const uintptr_t hal = MODE == MODE_DL ? 16 : al;
     return a.S % kpl == 0 && aligned(a.Bm, al) && aligned(a.Cm, al) &&
-           (MODE == MODE_DL || aligned(a.q, al)) && (!a.h0 || aligned(a.h0, al)) &&
-           (!a.h_last || aligned(a.h_last, al));
+           (MODE == MODE_DL || aligned(a.q, al)) && (!a.h0 || aligned(a.h0, hal)) &&
+           (!a.h_last || aligned(a.h_last, hal));
   };
   if constexpr (sizeof(T) == 2) {
     // Two states per lane fill the machine at config 3 (3072 waves, 12 per CU:
     // 2.34 ms against 2.74 with one state per lane). With fewer waves than that
     // (small batch x d_inner), one state per lane doubles the lanes: measured at
     // T 2048, D 1536, S 64: batch 1 1.063 -> 1.001 ms, batch 2 1.391 -> 1.340 ms.
-    const int64_t waves_kpl2 = a.batch * a.Dm * ((a.S + 1) / 2) / 64;
+    const int64_t waves_kpl2 = a.batch * a.n_chunks * a.Dm * ((a.S + 1) / 2) / 64;
     if (a.S <= 64 && waves_kpl2 < 12 * kCUs) return launch_ssm_kpl<T, MODE, 1>(a, s);
     // Four states per lane (32 bytes of B and C per lane and step, 384-thread
     // blocks, six steps in flight) for the inference walk: fewer k-sum and
@@ -648,7 +685,8 @@ int launch_ssm(const SsmArgs& a, hipStream_t s) {
     // form B4 T2048 d1536 4.66 -> 4.45 ms, B8 T1024 d1536 4.75 -> 4.57,
     // B4 T1024 d3072 4.51 -> 4.37, B2 T2048 d1536 2.34 -> 2.33; q form
     // B4 T1024 d1536 3.38 -> 3.26, B8 T512 d1536 3.46 -> 3.31.
-    if (a.S <= 64 && !a.h_ckpt && wide_ok(2) && a.batch * a.Dm * (a.S / 2) / 64 >= 6 * kCUs)
+    if (a.S <= 64 && !a.h_ckpt && wide_ok(2) &&
+        a.batch * a.n_chunks * a.Dm * (a.S / 2) / 64 >= 6 * kCUs)
       return launch_ssm_kpl<T, MODE, 2>(a, s);
     if (a.S <= 64) return launch_ssm_kpl<T, MODE, 1>(a, s);
     if (a.S <= 128 && wide_ok(2)) return launch_ssm_kpl<T, MODE, 2>(a, s);

@@ -114,8 +114,25 @@ def _dl_operands(delta, s, B, C, lambda_alpha, lambda_imag, D, h0):
     ops = [nat.aligned16(t.detach().to(dtype)) for t in (delta, s)]
     ops += [nat.aligned16(t.detach()) for t in (B, C)]
     ops += [nat.param_f32(t) for t in (lambda_alpha, lambda_imag, D)]
-    ops.append(None if h0 is None else nat.aligned16(h0.detach().to(dtype)))
+    # The state is fp32 at the boundary whatever the operands' dtype.
+    ops.append(None if h0 is None else nat.aligned16(h0.detach().float()))
     return ops
+
+
+# Largest d_state the backward kernel takes (one lane per state, a group of
+# d_state lanes per (b, d) inside one wave: include/mambaqc_hip.h,
+# mqc_ssm_fused_bwd). The inference walk goes to 256.
+SSM_BWD_MAX_STATE = 64
+
+
+def _require_trainable_state(B: torch.Tensor) -> None:
+    """Refuse, before any launch or allocation, a training forward whose
+    backward the library cannot run (d_state above SSM_BWD_MAX_STATE)."""
+    d_state = B.shape[-2] if B.dim() >= 2 else 0
+    if d_state > SSM_BWD_MAX_STATE:
+        raise ValueError(
+            f"ssm_forward_fused_dl: gradients need d_state <= {SSM_BWD_MAX_STATE} "
+            f"(got {d_state}); run without autograd (torch.no_grad) for inference")
 
 
 def ssm_fused_dl_train_forward(delta, s, B, C, lambda_alpha, lambda_imag, D, h0=None,
@@ -126,6 +143,7 @@ def ssm_fused_dl_train_forward(delta, s, B, C, lambda_alpha, lambda_imag, D, h0=
     Returns (y, h_last, saved) with saved = (delta, s, B, C, lambda_alpha,
     lambda_imag, D, h0, checkpoints) in the kernel's types.
     """
+    _require_trainable_state(B)
     batch, T, d_inner, d_state = _dl_check(delta, s, B, C, lambda_alpha, lambda_imag, D, h0)
     dl, sv, Bc, Cc, la, li, Dv, h0c = _dl_operands(delta, s, B, C, lambda_alpha, lambda_imag,
                                                    D, h0)
@@ -133,7 +151,7 @@ def ssm_fused_dl_train_forward(delta, s, B, C, lambda_alpha, lambda_imag, D, h0=
     K = nat.load().mqc_ssm_bwd_ckpt_every(code)
     n_ckpt = (T + K - 1) // K
     y = torch.empty(batch, T, d_inner, 4, device=Bc.device, dtype=Bc.dtype)
-    h_last = torch.empty(batch, d_inner, d_state, 4, device=Bc.device, dtype=Bc.dtype)
+    h_last = torch.empty(batch, d_inner, d_state, 4, device=Bc.device, dtype=torch.float32)
     ckpt = torch.empty(batch, max(n_ckpt, 1), d_inner, d_state, 4, device=Bc.device,
                        dtype=torch.float32)
     nat.call("mqc_ssm_fused_fwd_train", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
@@ -158,7 +176,7 @@ def ssm_fused_dl_backward(saved, gy, gh_last=None, eps: float = 1e-6):
         gy = torch.zeros(batch, T, d_inner, 4, device=dev, dtype=dtype)
     gy = nat.aligned16(gy.to(dtype))
     if gh_last is not None:
-        gh_last = nat.aligned16(gh_last.to(dtype))
+        gh_last = nat.aligned16(gh_last.float())
     d_delta = torch.empty(dl.shape, device=dev, dtype=torch.float32)
     d_s = torch.empty(sv.shape, device=dev, dtype=torch.float32)
     dB = torch.empty_like(Bc)
@@ -200,10 +218,49 @@ class _SsmFusedDL(torch.autograd.Function):
                 dD.to(t_D), None if dh0 is None else dh0.to(t_h0), None)
 
 
+def chunk_len_for(batch: int, seq_len: int, d_inner: int, d_state: int,
+                  dtype: torch.dtype) -> int:
+    """The chunk length the library picks for the inference walk at these sizes
+    (seq_len: no chunking, the whole walk)."""
+    code = nat.dtype_code(torch.empty(0, dtype=dtype))
+    L = int(nat.load().mqc_ssm_chunk_len_auto(batch, seq_len, d_inner, d_state, code))
+    if L < 0:
+        nat.check(L, "mqc_ssm_chunk_len_auto")
+    return L
+
+
+def _launch_dl_inference(dl, sv, Bc, Cc, la, li, Dv, h0c, eps, return_state, chunk_len):
+    batch, T, d_inner, d_state, _ = Bc.shape
+    dtype, dev = Bc.dtype, Bc.device
+    y = torch.empty(batch, T, d_inner, 4, device=dev, dtype=dtype)
+    h_last = (torch.empty(batch, d_inner, d_state, 4, device=dev, dtype=torch.float32)
+              if return_state else None)
+    code = nat.dtype_code(Bc)
+    if chunk_len is not None and int(chunk_len) < 1:
+        raise ValueError(f"ssm_forward_fused_dl: chunk_len must be >= 1, got {chunk_len}")
+    L = chunk_len_for(batch, T, d_inner, d_state, dtype) if chunk_len is None else int(chunk_len)
+    if 0 < L < T:
+        nbytes = int(nat.load().mqc_ssm_chunked_workspace_bytes(batch, T, d_inner, d_state, L))
+        if nbytes < 0:
+            nat.check(nbytes, "mqc_ssm_chunked_workspace_bytes")
+        ws = torch.empty(max(nbytes, 16), device=dev, dtype=torch.uint8)
+        nat.call("mqc_ssm_fused_fwd_chunked", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
+                 Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
+                 y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state, L, float(eps), code,
+                 ws.data_ptr(), nbytes, nat.stream_of(Bc))
+    else:
+        nat.call("mqc_ssm_fused_fwd", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
+                 Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
+                 y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state, float(eps), code,
+                 nat.stream_of(Bc))
+    return (y, h_last) if return_state else y
+
+
 def ssm_forward_fused_dl(delta: torch.Tensor, s: torch.Tensor, B: torch.Tensor,
                          C: torch.Tensor, lambda_alpha: torch.Tensor,
                          lambda_imag: torch.Tensor, D: torch.Tensor, eps: float = 1e-6,
-                         h0: torch.Tensor | None = None, return_state: bool = False):
+                         h0: torch.Tensor | None = None, return_state: bool = False,
+                         chunk_len: int | None = None):
     """The block's SSM with the Cayley discretisation fused in.
 
     delta, s: [batch, seq_len, d_inner]; B, C: [batch, seq_len, d_inner, d_state, 4];
@@ -211,26 +268,25 @@ def ssm_forward_fused_dl(delta: torch.Tensor, s: torch.Tensor, B: torch.Tensor,
     h0: optional [batch, d_inner, d_state, 4] initial state.
     Computes Lambda = (-softplus(lambda_alpha), tanh(lambda_imag)),
     q_t = Cayley(delta_t * Lambda, eps), and the recurrence with S = (s, 0, 0, 0).
-    Returns y [batch, seq_len, d_inner, 4] in B's dtype (and the final state if
-    return_state). Differentiable in every tensor argument when autograd is
-    recording (HIP backward, d_state <= 64); otherwise a single inference launch.
+    Returns y [batch, seq_len, d_inner, 4] in B's dtype (and the final state,
+    fp32 [batch, d_inner, d_state, 4], if return_state). The state is carried in
+    fp32 across calls as within one, so feeding a sequence in pieces from the
+    returned state gives the whole sequence's y.
+
+    Differentiable in every tensor argument when autograd is recording (HIP
+    backward, d_state <= 64). Otherwise one inference walk: whole, or, for
+    batches too small to fill the GPU, cut into chunks of `chunk_len` steps
+    walked side by side (None: the library's choice, chunk_len_for; an int
+    forces that length, >= seq_len meaning the whole walk).
     """
     inputs = (delta, s, B, C, lambda_alpha, lambda_imag, D) + ((h0,) if h0 is not None else ())
     if torch.is_grad_enabled() and any(t.requires_grad for t in inputs):
+        _require_trainable_state(B)
         y, h_last = _SsmFusedDL.apply(delta, s, B, C, lambda_alpha, lambda_imag, D, h0, eps)
         return (y, h_last) if return_state else y
-    batch, T, d_inner, d_state = _dl_check(delta, s, B, C, lambda_alpha, lambda_imag, D, h0)
-    dl, sv, Bc, Cc, la, li, Dv, h0c = _dl_operands(delta, s, B, C, lambda_alpha, lambda_imag,
-                                                   D, h0)
-    dtype = Bc.dtype
-    y = torch.empty(batch, T, d_inner, 4, device=Bc.device, dtype=dtype)
-    h_last = (torch.empty(batch, d_inner, d_state, 4, device=Bc.device, dtype=dtype)
-              if return_state else None)
-    nat.call("mqc_ssm_fused_fwd", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
-             Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
-             y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state, float(eps),
-             nat.dtype_code(Bc), nat.stream_of(Bc))
-    return (y, h_last) if return_state else y
+    _dl_check(delta, s, B, C, lambda_alpha, lambda_imag, D, h0)
+    ops = _dl_operands(delta, s, B, C, lambda_alpha, lambda_imag, D, h0)
+    return _launch_dl_inference(*ops, eps, return_state, chunk_len)
 
 
 def _front_operands(dt_raw, g_raw, x):
@@ -310,6 +366,7 @@ def ssm_forward_front_dl(dt_raw: torch.Tensor, g_raw: torch.Tensor, x: torch.Ten
     inputs = (dt_raw, g_raw, x, B, C, lambda_alpha, lambda_imag, D) + (
         (h0,) if h0 is not None else ())
     if torch.is_grad_enabled() and any(t.requires_grad for t in inputs):
+        _require_trainable_state(B)
         y, h_last = _SsmFrontFusedDL.apply(dt_raw, g_raw, x, B, C, lambda_alpha, lambda_imag,
                                            D, h0, eps)
         return (y, h_last) if return_state else y

@@ -175,7 +175,9 @@ def test_ssm_dl_backward_config3_slices():
         assert torch.isfinite(g1).all(), name
         assert_close(g2.float(), 2 * g1.float(), 2e-2, f"linearity {name}")
     del grads2
-    for b0, ds in ((0, slice(0, 2)), (3, slice(1534, 1536))):
+    # Both ends and the middle of the grid, in every batch row.
+    for b0, ds in ((0, slice(0, 2)), (1, slice(380, 382)), (2, slice(766, 768)),
+                   (3, slice(1150, 1152)), (3, slice(1534, 1536))):
         sl = [t[b0:b0 + 1, :, ds].detach().cpu().double() for t in (delta, s, Bm, C)]
         ref = [_leaf(t) for t in sl] + [_leaf(t[ds].detach().cpu().double()) for t in (la, li, D)]
         yr = oracle.ssm_forward_dl_reference(*ref)
@@ -316,14 +318,15 @@ def test_ssm_empty_sequence(dtype):
 
     y, hl = K.ssm_forward_fused_dl(*(t.to(DEV) for t in ins), h0=h0.to(DEV), return_state=True)
     assert y.shape == (b, 0, d, 4)
-    assert torch.equal(hl.cpu(), h0)
+    assert hl.dtype == torch.float32  # the state is fp32 at every storage dtype
+    assert torch.equal(hl.cpu(), h0.float())
     _, hl0 = K.ssm_forward_fused_dl(*(t.to(DEV) for t in ins), return_state=True)
     assert (hl0 == 0).all()
 
     got = [_leaf(t, DEV) for t in ins] + [_leaf(h0, DEV)]
     y, hl = K.ssm_forward_fused_dl(*got[:7], h0=got[7], return_state=True)
     (hl.float() * gh.to(DEV).float()).sum().backward()
-    assert torch.equal(hl.detach().cpu(), h0)
+    assert torch.equal(hl.detach().cpu(), h0.float())
     assert torch.equal(got[7].grad.cpu(), gh)
     for t, name in zip(got[4:7], ["lambda_alpha", "lambda_imag", "D"]):
         assert t.grad is not None and (t.grad == 0).all(), name

@@ -314,27 +314,48 @@ def test_ssm_front_unaligned_views():
     assert torch.equal(d1, d2) and torch.equal(s1, s2)
 
 
-@pytest.mark.parametrize("shape,dtype", [((2, 40, 6, 64), torch.float32),
-                                         # several states per lane (2 in fp32, 4 in bf16)
-                                         ((8, 20, 768, 64), torch.float32),
-                                         ((8, 20, 768, 64), torch.bfloat16)])
-def test_ssm_fused_dl_state_carry(shape, dtype):
-    """Running [0, T) equals running [0, t1) then [t1, T) from the carried state
-    (exactly in fp32, where the state is carried in fp32; to the 16-bit
-    tolerance in bf16, where h_last is stored in bf16)."""
+@pytest.mark.parametrize("shape,dtype,small", [((2, 40, 6, 64), torch.float32, False),
+                                               # several states per lane (2 in fp32, 4 in bf16)
+                                               ((8, 20, 768, 64), torch.float32, False),
+                                               ((8, 20, 768, 64), torch.bfloat16, False),
+                                               # long walks with slow decay in 16-bit storage
+                                               ((2, 300, 64, 64), torch.bfloat16, True),
+                                               ((2, 300, 64, 64), torch.float16, True),
+                                               ((8, 260, 768, 64), torch.bfloat16, True)])
+def test_ssm_fused_dl_state_carry(shape, dtype, small):
+    """Running [0, T) equals running it in pieces from the carried state, bit
+    for bit in every storage dtype: the state crosses the call boundary in
+    fp32, the precision the walk carries it in. The `small` cases take steps
+    delta ~ 0.01 (|q| within about 1 % of 1), where a state rounded to 16 bits
+    at every boundary (a recurrent decode) would drift by about 1/(1 - |q|)
+    times its rounding error; pieces include single steps."""
     a = _dl_inputs(*shape, seed=41, dtype=dtype)
+    if small:
+        a = (a[0].float().mul(0.08).to(dtype),) + a[1:]
     dev = [t.to(DEV) for t in a]
     delta, s, Bm, C, la, li, D = dev
-    y_full, h_full = K.ssm_forward_fused_dl(*dev, return_state=True)
-    y1, h1 = K.ssm_forward_fused_dl(delta[:, :15], s[:, :15], Bm[:, :15], C[:, :15], la, li, D,
-                                    return_state=True)
-    y2, h2 = K.ssm_forward_fused_dl(delta[:, 15:], s[:, 15:], Bm[:, 15:], C[:, 15:], la, li, D,
-                                    h0=h1, return_state=True)
-    t_carry = 1e-5 if dtype == torch.float32 else tol(dtype)
-    assert_close(torch.cat([y1, y2], 1), y_full, t_carry, "carry y")
-    assert_close(h2, h_full, t_carry, "carry h")
+    T = shape[1]
+    # Whole walks (no time chunks) everywhere: the same arithmetic step by step.
+    whole = dict(chunk_len=1 << 30)
+    y_full, h_full = K.ssm_forward_fused_dl(*dev, return_state=True, **whole)
+    assert h_full.dtype == torch.float32
+    cuts = [0, 15, 16, 17, T // 2, T] if T > 40 else [0, 15, T]
+    h, ys = None, []
+    for t0, t1 in zip(cuts[:-1], cuts[1:]):
+        y, h = K.ssm_forward_fused_dl(delta[:, t0:t1], s[:, t0:t1], Bm[:, t0:t1], C[:, t0:t1],
+                                      la, li, D, h0=h, return_state=True, **whole)
+        ys.append(y)
+    assert torch.equal(torch.cat(ys, 1), y_full), "pieces differ from the whole walk"
+    assert torch.equal(h, h_full), "final state of the pieces differs"
+    # The library's own choice (time chunks where the batch is small) agrees
+    # to rounding.
+    y_auto, h_auto = K.ssm_forward_fused_dl(*dev, return_state=True)
+    assert_close(y_auto, y_full, tol(dtype), "auto walk vs whole walk")
+    assert_close(h_auto, h_full, 1e-4, "auto walk state vs whole walk")
     ref_y, ref_h = oracle.ssm_forward_dl_reference(*(up(t) for t in a), return_state=True)
     assert_close(y_full, ref_y, tol(dtype), "y vs oracle")
+    # The state is fp32 at every dtype: compare it at the fp32 tolerance where
+    # the operands were fp32, at the 16-bit one otherwise (inputs rounded).
     assert_close(h_full, ref_h, tol(dtype), "final state vs oracle")
 
 
@@ -357,7 +378,10 @@ def test_ssm_fused_dl_config3_full_size():
     y = K.ssm_forward_fused_dl(delta, s, Bm, C, la, li, D)
     y2 = K.ssm_forward_fused_dl(delta, (2 * s.float()).to(bf), Bm, C, la, li, D)
     assert_close(y2.float(), 2 * y.float(), 2e-2, "linearity in s")
-    for b0, ds in ((0, slice(0, 3)), (3, slice(1533, 1536))):
+    # Slices at both ends and in the middle of the grid, in every batch row
+    # (each (b, d-block) is its own workgroup).
+    for b0, ds in ((0, slice(0, 3)), (1, slice(380, 383)), (2, slice(766, 769)),
+                   (3, slice(1150, 1153)), (0, slice(767, 768)), (3, slice(1533, 1536))):
         want = oracle.ssm_forward_dl_reference(
             up(delta[b0:b0 + 1, :, ds]), up(s[b0:b0 + 1, :, ds]), up(Bm[b0:b0 + 1, :, ds]),
             up(C[b0:b0 + 1, :, ds]), up(la[ds]), up(li[ds]), up(D[ds]))
@@ -439,6 +463,31 @@ def test_block_bf16_vs_oracle():
         got = blk.to(DEV)(x.to(DEV))
     assert got.dtype == torch.bfloat16
     assert_close(got, want, 2e-2, "block bf16")
+
+
+def test_block_headline_width_bf16_vs_oracle():
+    """The headline configuration's block (d_model 768, d_state 64, expand 2:
+    d_inner 1536) in bf16 at B4 T256 against the oracle in fp32 on the same
+    bf16-rounded weights and input. 1024 token rows make the B/C projections
+    take wide_linear's column blocks (1.2 GB of weight each), and the SSM takes
+    the inference walk with four states per lane (384-thread blocks): the
+    composition the benchmark times."""
+    from mambaqc_amd.layers import quaternion_linear as ql
+
+    torch.manual_seed(11)
+    with torch.device(DEV):
+        blk = mambaqc_amd.QuaternionMamba2Block(768, d_state=64, d_conv=4, expand_factor=2)
+    blk = blk.to(torch.bfloat16)
+    x = torch.randn(4, 256, 768, generator=torch.Generator(device=DEV).manual_seed(12),
+                    device=DEV).to(torch.bfloat16)
+    n, k = blk.B_proj.weight.shape
+    assert len(ql._blocks(n, k, 2)) > 1 and x.numel() // 768 >= ql.WIDE_LINEAR_MIN_ROWS
+    with torch.no_grad():
+        got = blk(x)
+    assert got.dtype == torch.bfloat16
+    sd = {kk: v.detach().float().cpu() for kk, v in blk.state_dict().items()}
+    want = oracle.block_forward_reference(sd, x.float().cpu(), d_state=64)
+    assert_close(got, want, 2e-2, "block d768 s64 e2 bf16")
 
 
 def test_block_built_under_inference_mode():

@@ -69,6 +69,23 @@ def test_lm_state_pieces_equal_whole():
     assert_close(torch.cat(parts, 1), whole, 1e-4, "pieces vs whole")
 
 
+def test_lm_state_pieces_equal_whole_bf16():
+    """As above in bf16 over a longer walk (T 260, one single-token piece): the
+    recurrent state crosses each call in fp32, so the pieces differ from the
+    whole only by the GEMMs' rounding of each token, not by a state rounded
+    to 16 bits at every boundary."""
+    lm = _tiny(seed=8, d_state=16).to(DEV).to(torch.bfloat16)
+    ids = torch.randint(0, 37, (2, 260), generator=torch.Generator().manual_seed(9)).to(DEV)
+    with torch.no_grad():
+        whole = lm(ids)["logits"]
+        states, parts = None, []
+        for a, b in ((0, 100), (100, 101), (101, 260)):
+            logits, states = lm.forward_with_state(ids[:, a:b], states)
+            parts.append(logits)
+    assert all(st[1].dtype == torch.float32 for st in states)
+    assert_close(torch.cat(parts, 1), whole, 2e-2, "bf16 pieces vs whole")
+
+
 def test_generate_matches_full_recompute():
     """Recurrent generation gives the tokens of the reference's rule (full
     forward over the whole sequence per new token); greedy via top_k=1."""

@@ -24,25 +24,25 @@ FAKE = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
 
 def declared_symbols():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:const char\*|int)\s+(mqc_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int64_t|int)\s+(mqc_\w+)\(", text, re.M)))
 
 
 def test_header_declares_the_api():
     names = declared_symbols()
-    assert len(names) == 22, names
-    assert set(nat.SIGNATURES) <= set(names)
+    assert len(names) == 25, names
+    assert set(nat.SIGNATURES) | set(nat.SIGNATURES_I64) <= set(names)
 
 
 def test_library_exports_every_declared_symbol():
     lib = nat.load()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mqc_abi_version() == nat.ABI_VERSION == 3
+    assert lib.mqc_abi_version() == nat.ABI_VERSION == 4
 
 
 def test_status_strings():
     assert nat.status_string(0) == "ok"
-    for code in (-1, -2, -3, -4, -5):
+    for code in (-1, -2, -3, -4, -5, -6):
         s = nat.status_string(code)
         assert s and s != "unknown status"
 
@@ -112,6 +112,24 @@ def test_block_training_forward_refuses_cpu():
         blk(torch.zeros(1, 3, 8))
 
 
+def test_training_forward_refuses_d_state_above_backward_limit():
+    """A recorded forward with d_state > 64 fails at once with a clear error
+    (before any launch or allocation), not inside backward after the whole
+    training forward has run; d_state 64 passes the check and reaches the
+    device check."""
+    from mambaqc_amd.kernels.ssm_fused import SSM_BWD_MAX_STATE
+
+    assert SSM_BWD_MAX_STATE == 64
+    for fn, lead in ((K.ssm_forward_fused_dl, 2), (K.ssm_forward_front_dl, 3)):
+        for d_state, err in ((65, ValueError), (64, RuntimeError)):
+            b, t, d = 1, 3, 2
+            args = [torch.zeros(b, t, d, requires_grad=True) for _ in range(lead)]
+            args += [torch.zeros(b, t, d, d_state, 4), torch.zeros(b, t, d, d_state, 4),
+                     torch.zeros(d, d_state), torch.zeros(d, d_state, 3), torch.zeros(d)]
+            with pytest.raises(err, match="d_state <= 64" if err is ValueError else "ROCm"):
+                fn(*args)
+
+
 def test_training_validation_codes_without_gpu():
     lib = nat.load()
     assert lib.mqc_ssm_bwd_ckpt_every(0) == 4
@@ -136,6 +154,43 @@ def test_training_validation_codes_without_gpu():
     assert lib.mqc_qln_bwd(None, None, None, None, None, None, None, 0, 4, 1e-5, 0, None) == 0
     # Gate backward: dz narrower than the gated columns.
     assert lib.mqc_out_gate_bwd(FAKE, FAKE, 8, FAKE, FAKE, FAKE, 2, 8, 4, 0, None) == -2
+
+
+def test_chunk_policy_and_workspace_without_gpu():
+    """The library's chunk choice for the inference walk: none where
+    batch * d_inner * d_state states come near filling the GPU (config 3's
+    393 216 states, or half of them) or the walk is short; chunks of at least
+    64 steps, at most 8 of them, more for fewer states.
+    The workspace size formula, and the chunked entry point's validation."""
+    from mambaqc_amd.kernels.ssm_fused import chunk_len_for
+
+    bf = torch.bfloat16
+    assert chunk_len_for(4, 2048, 1536, 64, bf) == 2048
+    assert chunk_len_for(1, 100, 1536, 64, bf) == 100
+    assert chunk_len_for(1, 2048, 1536, 128, bf) == 2048  # d_state > 64: whole walk
+    L = chunk_len_for(1, 2048, 1536, 64, bf)
+    assert 64 <= L < 2048 and -(-2048 // L) <= 8
+    # Measured slower with chunks: batch 2, and d_state 16 at batch 4.
+    assert chunk_len_for(2, 2048, 1536, 64, bf) == 2048
+    assert chunk_len_for(4, 2048, 1536, 16, bf) == 2048
+    L8 = chunk_len_for(1, 2048, 768, 64, bf)
+    assert 64 <= L8 < L and -(-2048 // L8) <= 8
+    lib = nat.load()
+    assert lib.mqc_ssm_chunked_workspace_bytes(1, 2048, 1536, 64, 512) == 24 * 3 * 1536 * 64
+    assert lib.mqc_ssm_chunked_workspace_bytes(2, 10, 3, 4, 10) == 0
+    assert lib.mqc_ssm_chunked_workspace_bytes(2, 10, 3, 4, 0) == -2
+    assert lib.mqc_ssm_chunk_len_auto(1, 8, 1, 1, 9) == -3
+    P = [FAKE] * 7
+    need = lib.mqc_ssm_chunked_workspace_bytes(1, 100, 4, 8, 10)
+    # chunk_len 0; workspace missing, too small; d_state above the chunked limit.
+    assert lib.mqc_ssm_fused_fwd_chunked(*P, None, FAKE, None, 1, 100, 4, 8, 0, 1e-6, 1,
+                                         FAKE, need, None) == -2
+    assert lib.mqc_ssm_fused_fwd_chunked(*P, None, FAKE, None, 1, 100, 4, 8, 10, 1e-6, 1,
+                                         None, need, None) == -1
+    assert lib.mqc_ssm_fused_fwd_chunked(*P, None, FAKE, None, 1, 100, 4, 8, 10, 1e-6, 1,
+                                         FAKE, need - 1, None) == -6
+    assert lib.mqc_ssm_fused_fwd_chunked(*P, None, FAKE, None, 1, 100, 4, 65, 10, 1e-6, 1,
+                                         FAKE, 1 << 40, None) == -5
 
 
 def test_step_counter_limits_without_gpu():
