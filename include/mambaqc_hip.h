@@ -14,7 +14,9 @@
  *   - The return value is MQC_OK (0), a negative MQC_E_* code when argument
  *     validation fails (checked before any HIP call, so these are safe to
  *     probe without a GPU), or a positive hipError_t from the launch.
- *   - No global mutable state: calls are re-entrant and thread-safe.
+ *   - No global mutable state: calls are re-entrant and thread-safe. The one
+ *     exception is mqc_ssm_fused_fwd_chunked_noalloc (a fixed device array
+ *     shared by its calls on one device).
  *
  * Each function names the reference interface (polux06/mambaqc) it replaces.
  */
@@ -151,6 +153,28 @@ int mqc_ssm_fused_fwd_chunked(const void* delta, const void* s, const void* B, c
                               int64_t seq_len, int64_t d_inner, int64_t d_state,
                               int64_t chunk_len, float eps, int dtype, void* workspace,
                               int64_t workspace_bytes, void* stream);
+
+/* mqc_ssm_fused_fwd_chunked without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * The chunk transitions go to a fixed device array inside the library,
+ * mqc_ssm_chunked_scratch_bytes() bytes (32 MiB) on every device the library
+ * runs on, held until the process ends; a call whose
+ * mqc_ssm_chunked_workspace_bytes exceeds it returns MQC_E_SPACE before any
+ * HIP call. Nothing is allocated or freed. Every call on one device uses the
+ * same array, so calls that overlap on one device (concurrent streams,
+ * threads) race: serialise them. No contents are needed on entry (every
+ * transition is written before it is read). Otherwise as
+ * mqc_ssm_fused_fwd_chunked. */
+int mqc_ssm_fused_fwd_chunked_noalloc(const void* delta, const void* s, const void* B,
+                                      const void* C, const float* lambda_alpha,
+                                      const float* lambda_imag, const float* D, const void* h0,
+                                      void* y, void* h_last, int64_t batch, int64_t seq_len,
+                                      int64_t d_inner, int64_t d_state, int64_t chunk_len,
+                                      float eps, int dtype, void* stream);
+
+/* Size in bytes of the fixed device scratch of mqc_ssm_fused_fwd_chunked_noalloc. */
+int64_t mqc_ssm_chunked_scratch_bytes(void);
 
 /* Quaternion LayerNorm over the d axis of each of `rows` rows of d quaternions:
  *   n = sqrt(|q|^2 + eps); mu, var = mean and biased variance of n over d;

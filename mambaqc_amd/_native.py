@@ -57,6 +57,8 @@ SIGNATURES = {
                                  _i64, _i64, _int, _vp],
     "mqc_ssm_fused_fwd_chunked": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp, _i64, _vp],
+    "mqc_ssm_fused_fwd_chunked_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                          _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp],
 }
 
 # name -> argtypes of the entry points that return int64_t (a size, or a
@@ -64,6 +66,7 @@ SIGNATURES = {
 SIGNATURES_I64 = {
     "mqc_ssm_chunk_len_auto": [_i64, _i64, _i64, _i64, _int],
     "mqc_ssm_chunked_workspace_bytes": [_i64, _i64, _i64, _i64, _i64],
+    "mqc_ssm_chunked_scratch_bytes": [],
 }
 
 ABI_VERSION = 4

@@ -426,7 +426,7 @@ const char* mqc_status_string(int status) {
     case MQC_E_DTYPE: return "unknown dtype code";
     case MQC_E_ALIGN: return "a pointer is not aligned for the kernel's vector loads";
     case MQC_E_LIMIT: return "a size is beyond what the kernels support";
-    case MQC_E_SPACE: return "the workspace is smaller than the call needs";
+    case MQC_E_SPACE: return "the workspace (or the library's fixed scratch) is smaller than the call needs";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
   }
 }

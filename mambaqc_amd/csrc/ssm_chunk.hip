@@ -1,9 +1,42 @@
 // C ABI of the time-chunked fused SSM walk (kernels and launches: ssm_chunk.hpp).
+#include <mutex>
+
 #include "ssm_chunk.hpp"
 
 using namespace mqc;
 
+// Fixed device scratch of mqc_ssm_fused_fwd_chunked_noalloc: the chunk
+// transitions live here instead of in a caller's workspace. Each device the
+// library runs on holds its own copy for the life of the process. In host code
+// `scratch` names a host-side stand-in, never the device memory: the device
+// address comes from hipGetSymbolAddress, once per device (scratch_ptr).
+constexpr int64_t kScratchBytes = (int64_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up on the first call on
+// each device, with that device current).
+int scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return MQC_E_LIMIT;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return (int)hipErrorInvalidSymbol;
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return MQC_OK;
+}
 
 // Chunks are at least this long: each chunk pays one extra walk over its
 // delta, s and B (the carry launch) and a short prefix launch.
@@ -109,6 +142,32 @@ int mqc_ssm_fused_fwd_chunked(const void* delta, const void* s, const void* B, c
     case MQC_BF16: return run_chunked<bf16_t>(a, (float*)workspace, hs);
     default: return run_chunked<f16_t>(a, (float*)workspace, hs);
   }
+}
+
+int64_t mqc_ssm_chunked_scratch_bytes(void) { return kScratchBytes; }
+
+int mqc_ssm_fused_fwd_chunked_noalloc(const void* delta, const void* s, const void* B,
+                                      const void* C, const float* lambda_alpha,
+                                      const float* lambda_imag, const float* D, const void* h0,
+                                      void* y, void* h_last, int64_t batch, int64_t seq_len,
+                                      int64_t d_inner, int64_t d_state, int64_t chunk_len,
+                                      float eps, int dtype, void* stream) {
+  bool nothing;
+  int st = check_chunked(delta, s, B, C, lambda_alpha, lambda_imag, D, y, h_last, batch, seq_len,
+                         d_inner, d_state, chunk_len, dtype, nothing);
+  if (st != MQC_OK || nothing) return st;
+  const int64_t nc = seq_len > chunk_len ? (seq_len + chunk_len - 1) / chunk_len : 1;
+  if (nc > 1 && d_state > kChunkMaxState) return MQC_E_LIMIT;
+  const int64_t need = ssm_chunk_workspace_bytes(batch, seq_len, d_inner, d_state, chunk_len);
+  if (need > kScratchBytes) return MQC_E_SPACE;
+  void* ws = nullptr;
+  if (nc > 1) {
+    st = scratch_ptr(&ws);
+    if (st != MQC_OK) return st;
+  }
+  return mqc_ssm_fused_fwd_chunked(delta, s, B, C, lambda_alpha, lambda_imag, D, h0, y, h_last,
+                                   batch, seq_len, d_inner, d_state, chunk_len, eps, dtype, ws,
+                                   kScratchBytes, stream);
 }
 
 }  // extern "C"
