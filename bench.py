@@ -1,6 +1,7 @@
 """Benchmark: QuaternionMamba2Block forward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--mode full|ssm|ssm_bwd|cumprod|cayley|qln|copy]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+                    [--mode full|ssm|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|decode|train|copy]
 
 Workload (BASELINE configs[2]/[3] shape): one QuaternionMamba2Block forward,
 batch 4, seq_len 2048, d_model 768, d_state 64, d_conv 4, expand_factor 2
@@ -216,6 +217,19 @@ def read_traffic():
     return None
 
 
+def nat_aligned(t):
+    from mambaqc_amd import _native as nat
+    return nat.aligned16(t)
+
+
+def mqc_gemm(x, w, out):
+    """out = x @ w.T through the library's MFMA GEMM (bf16)."""
+    from mambaqc_amd import _native as nat
+    nat.call("mqc_gemm_nt", x, x.data_ptr(), w.data_ptr(), out.data_ptr(), x.shape[0],
+             w.shape[0], x.shape[1], nat.BF16, nat.stream_of(x))
+    return out
+
+
 def box_copy_gbs(reps=20):
     """Read+write bandwidth of a 1 GiB device-to-device copy on this box. HBM
     throughput differs from box to box by up to ~15 %; this puts the SSM's
@@ -278,6 +292,16 @@ def run_full(args):
         stages["qln"] = event_time_ms(lambda: blk.norm(y), 10)
         stages["B_proj+C_proj GEMMs"] = event_time_ms(lambda: (blk.B_proj(s), blk.C_proj(s)), 5)
         del y
+        # A/B of the B projection alone: hipBLASLt (column blocks, the block's
+        # path) against this library's MFMA GEMM (mqc_gemm_nt), same operands.
+        xa = nat_aligned(s.reshape(-1, DI))
+        wb = blk.B_proj.weight.detach()
+        gemm_out = torch.empty(xa.shape[0], wb.shape[0], device="cuda", dtype=dtype)
+        stages["B_proj GEMM hipBLASLt (column blocks)"] = event_time_ms(
+            lambda: blk.B_proj(s), 5)
+        stages["B_proj GEMM mqc_gemm_nt (MFMA, this library)"] = event_time_ms(
+            lambda: mqc_gemm(xa, wb, gemm_out), 5)
+        del gemm_out, xa
     qln_gbs = qln_bytes(B * T, DI) / (stages["qln"] * 1e-3) / 1e9
     del delta, s, Bq, Cq
     torch.cuda.empty_cache()
@@ -535,6 +559,21 @@ def run_kernel_loop(args):
                     with torch.autocast("cuda", dtype=torch.float16):
                         loss = blk(x).float().pow(2).mean()
                     (loss * 2.0 ** 16).backward()
+            nbytes = 0
+        elif args.mode == "gemm":
+            # The config-3 B projection through the library's MFMA GEMM.
+            bf = torch.bfloat16
+            x = torch.randn(B * T, DI, generator=g, device="cuda").to(bf)
+            w = (torch.randn(DI * DS * 4, DI, generator=g, device="cuda") * 0.02).to(bf)
+            out = torch.empty(B * T, DI * DS * 4, device="cuda", dtype=bf)
+            fn = lambda: mqc_gemm(x, w, out)
+            nbytes = 0
+        elif args.mode == "gemm_hipblaslt":
+            from mambaqc_amd.layers.quaternion_linear import wide_linear
+            bf = torch.bfloat16
+            x = torch.randn(B * T, DI, generator=g, device="cuda").to(bf)
+            w = (torch.randn(DI * DS * 4, DI, generator=g, device="cuda") * 0.02).to(bf)
+            fn = lambda: wide_linear(x, w)
             nbytes = 0
         elif args.mode == "copy":
             src = torch.empty(1 << 28, device="cuda")  # 1 GiB

@@ -176,6 +176,16 @@ int mqc_ssm_fused_fwd_chunked_noalloc(const void* delta, const void* s, const vo
 /* Size in bytes of the fixed device scratch of mqc_ssm_fused_fwd_chunked_noalloc. */
 int64_t mqc_ssm_chunked_scratch_bytes(void);
 
+/* C[M, N] = X[M, K] . W[N, K]^T in bf16 with fp32 accumulation (dtype must be
+ * MQC_BF16), contiguous row-major X, W, C, 16-byte aligned; N a multiple of
+ * 256, K of 64, M any. The hand-written MFMA GEMM of the block's B/C
+ * projections (F.linear, mambaqc/layers/quaternion_linear.py:145-161, called
+ * at mambaqc/models/quaternion_mamba2_block.py:186-191), the first stage of
+ * fusing them with the SSM walk; the block itself keeps hipBLASLt, which is
+ * faster at the config-3 shape. */
+int mqc_gemm_nt(const void* X, const void* W, void* C, int64_t M, int64_t N, int64_t K, int dtype,
+                void* stream);
+
 /* Quaternion LayerNorm over the d axis of each of `rows` rows of d quaternions:
  *   n = sqrt(|q|^2 + eps); mu, var = mean and biased variance of n over d;
  *   out = gamma * (n - mu) / sqrt(var + eps) * q / (n + eps) + beta.

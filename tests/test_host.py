@@ -29,7 +29,7 @@ def declared_symbols():
 
 def test_header_declares_the_api():
     names = declared_symbols()
-    assert len(names) == 27, names
+    assert len(names) == 28, names
     assert set(nat.SIGNATURES) | set(nat.SIGNATURES_I64) <= set(names)
 
 
@@ -191,6 +191,17 @@ def test_chunk_policy_and_workspace_without_gpu():
                                          FAKE, need - 1, None) == -6
     assert lib.mqc_ssm_fused_fwd_chunked(*P, None, FAKE, None, 1, 100, 4, 65, 10, 1e-6, 1,
                                          FAKE, 1 << 40, None) == -5
+
+
+def test_gemm_validation_without_gpu():
+    lib = nat.load()
+    # bf16 only; N a multiple of 256, K of 64; nothing to do is not an error.
+    assert lib.mqc_gemm_nt(FAKE, FAKE, FAKE, 8, 256, 64, 0, None) == -3
+    assert lib.mqc_gemm_nt(FAKE, FAKE, FAKE, 8, 200, 64, 1, None) == -2
+    assert lib.mqc_gemm_nt(FAKE, FAKE, FAKE, 8, 256, 96, 1, None) == -2
+    assert lib.mqc_gemm_nt(None, FAKE, FAKE, 8, 256, 64, 1, None) == -1
+    assert lib.mqc_gemm_nt(ctypes.c_void_p(4104), FAKE, FAKE, 8, 256, 64, 1, None) == -4
+    assert lib.mqc_gemm_nt(None, None, None, 0, 256, 64, 1, None) == 0
 
 
 def test_step_counter_limits_without_gpu():
