@@ -1,7 +1,7 @@
 """Benchmark: QuaternionMamba2Block forward on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
-                    [--mode full|ssm|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|decode|train|copy]
+                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|decode|train|copy]
 
 Workload (BASELINE configs[2]/[3] shape): one QuaternionMamba2Block forward,
 batch 4, seq_len 2048, d_model 768, d_state 64, d_conv 4, expand_factor 2
@@ -494,17 +494,21 @@ def run_kernel_loop(args):
     g = torch.Generator(device="cuda").manual_seed(0)
     reps = args.steps
     with torch.inference_mode():
-        if args.mode == "ssm":
+        if args.mode in ("ssm", "ssm_b1", "ssm_b1_whole"):
+            # ssm: config 3 (B4). ssm_b1: batch 1 with the library's choice of
+            # time chunks; ssm_b1_whole: batch 1 as one whole walk.
+            bb = B if args.mode == "ssm" else 1
             bf = torch.bfloat16
-            delta = torch.nn.functional.softplus(torch.randn(B, T, DI, generator=g, device="cuda") - 2).to(bf)
-            s = torch.randn(B, T, DI, generator=g, device="cuda").to(bf)
-            Bq = torch.randn(B, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
-            Cq = torch.randn(B, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
+            delta = torch.nn.functional.softplus(torch.randn(bb, T, DI, generator=g, device="cuda") - 2).to(bf)
+            s = torch.randn(bb, T, DI, generator=g, device="cuda").to(bf)
+            Bq = torch.randn(bb, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
+            Cq = torch.randn(bb, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
             la = torch.randn(DI, DS, generator=g, device="cuda") * 0.5 + 1
             li = torch.randn(DI, DS, 3, generator=g, device="cuda") * 0.1
             Dv = torch.ones(DI, device="cuda")
-            fn = lambda: K.ssm_forward_fused_dl(delta, s, Bq, Cq, la, li, Dv)
-            nbytes = ssm_bytes(B, T, DI, DS)
+            L = T if args.mode == "ssm_b1_whole" else None
+            fn = lambda: K.ssm_forward_fused_dl(delta, s, Bq, Cq, la, li, Dv, chunk_len=L)
+            nbytes = ssm_bytes(bb, T, DI, DS)
         elif args.mode == "ssm_bwd":
             from mambaqc_amd.kernels.ssm_fused import (ssm_fused_dl_backward,
                                                        ssm_fused_dl_train_forward)

@@ -159,9 +159,17 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int j = tid & (G - 1);
-  // Hardware block order. The XCD remap of the forward (xcd_block) cuts this
-  // kernel's reads from 1.077x to 1.012x the algorithmic bytes (neighbouring
-  // d-blocks share lines of delta, s and gy) but measured 1.6 % slower.
+  // Hardware block order. Neighbouring d-blocks share 128-byte lines of delta,
+  // s and gy, and the hardware hands them to different XCDs, each of which
+  // fetches the line: measured on MI355X (rocprofv3, config 3, bf16) reads at
+  // 1.086x the algorithmic bytes in this order against 1.032x with the
+  // forward's XCD remap (xcd_block) and 512-thread blocks, whose L2 then holds
+  // a whole line. The remap still measured slower (5.92 ms here; 5.99 remapped,
+  // 6.34 with 512 threads, 6.14 with both, same buffers): the kernel runs at
+  // the box's copy rate, and the 4 % fewer reads do not buy back the order.
+  // The write excess (1.024x) is the fp32 d_delta / d_s rows: a block holds 4
+  // d's, 16 bytes of each row, which leave the L2 as 12.6 M masked 32-byte
+  // writes (TCC_EA0_WRREQ minus TCC_EA0_WRREQ_64B), 0.44 GB for 0.1 GB of data.
   const int64_t b = blockIdx.y;
   const int64_t d_raw = (int64_t)blockIdx.x * GPB + tid / G;
   const bool gvalid = d_raw < a.Dm;
