@@ -1,7 +1,8 @@
 """Benchmark: QuaternionMamba2Block forward on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
-                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|decode|train|copy]
+                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|decode|decode_graph|train|copy]
+                    [--preset small|base|large]
 
 Workload (BASELINE configs[2]/[3] shape): one QuaternionMamba2Block forward,
 batch 4, seq_len 2048, d_model 768, d_state 64, d_conv 4, expand_factor 2
@@ -477,13 +478,20 @@ def lm_timing(args):
         lm._forward_with_state(tok, states)
         dec_ms = event_time_ms(lambda: lm._forward_with_state(tok, states), 20)
     log(f"config 5 recurrent decode: {dec_ms:.2f} ms per step of {B} tokens")
-    del lm, states
+    from mambaqc_amd.lm import DecodeGraph
+    with torch.no_grad():
+        graph = DecodeGraph(lm, states)
+        graph.step(tok)
+        dec_graph_ms = event_time_ms(lambda: graph.step(tok), 20)
+    log(f"config 5 recurrent decode as a HIP graph: {dec_graph_ms:.2f} ms per step")
+    del lm, states, graph
     torch.cuda.empty_cache()
     return {"workload": "QuaternionMamba2 base (12 layers) forward, bf16, B4 T2048, vocab 10000",
             "params": n_params, "ms_per_step": round(ms, 2),
             "tokens_per_s": round(B * T / ms * 1e3, 1),
             "decode_ms_per_token_step": round(dec_ms, 3),
-            "decode_tokens_per_s": round(B / dec_ms * 1e3, 1)}
+            "decode_tokens_per_s": round(B / dec_ms * 1e3, 1),
+            "decode_graph_ms_per_token_step": round(dec_graph_ms, 3)}
 
 
 def run_kernel_loop(args):
@@ -536,18 +544,26 @@ def run_kernel_loop(args):
             bt = torch.zeros(DI, 4, device="cuda")
             fn = lambda: K.quaternion_layer_norm_fused(y, gm, bt)
             nbytes = qln_bytes(B * T, DI)
-        elif args.mode == "decode":
-            # Recurrent decoding with the base preset: prompt of 64 tokens, then
-            # one step per token through every block (bf16, batch 4).
+        elif args.mode in ("decode", "decode_graph"):
+            # Recurrent decoding with a preset (--preset, base by default):
+            # prompt of 64 tokens, then one step per token through every block
+            # (bf16, batch 4); decode_graph replays the step as a HIP graph.
             import mambaqc_amd
+            from mambaqc_amd.lm import DecodeGraph
             torch.manual_seed(0)
+            build = getattr(mambaqc_amd, f"quaternion_mamba2_{args.preset}")
             # Parameters built outside inference mode, as in lm_timing.
             with torch.inference_mode(False), torch.device("cuda"):
-                lm = mambaqc_amd.quaternion_mamba2_base(10000).to(torch.bfloat16).eval()
+                lm = build(10000).to(torch.bfloat16).eval()
             ids = torch.randint(0, 10000, (B, 64), generator=g, device="cuda")
             _, states = lm.forward_with_state(ids)
             tok = ids[:, -1:]
-            fn = lambda: lm._forward_with_state(tok, states)
+            if args.mode == "decode":
+                fn = lambda: lm._forward_with_state(tok, states)
+            else:
+                with torch.inference_mode(False), torch.no_grad():
+                    graph = DecodeGraph(lm, states)
+                fn = lambda: graph.step(tok)
             nbytes = sum(p.numel() * p.element_size() for p in lm.parameters())
         elif args.mode == "train":
             # Config 4: block forward + backward under fp16 autocast, loss
@@ -599,6 +615,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--mode", default="full")
+    ap.add_argument("--preset", default="base", choices=["small", "base", "large"],
+                    help="LM preset of the decode modes")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--block-only", action="store_true",
                     help="skip the config-4 and config-5 legs (for a kernel trace of the block)")

@@ -112,14 +112,19 @@ class QuaternionMamba2(nn.Module):
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 100,
                  temperature: float = 1.0, top_k: int | None = None,
-                 top_p: float | None = None) -> torch.Tensor:
+                 top_p: float | None = None, use_graph: bool = False) -> torch.Tensor:
         """Autoregressive sampling with the reference's rules (:169-227):
         temperature, then top-k, then nucleus (top-p) filtering, then one
-        torch.multinomial draw per sequence per step."""
+        torch.multinomial draw per sequence per step.
+
+        use_graph: run the decode steps as replays of one captured HIP graph
+        (DecodeGraph) instead of launching every kernel from Python; the same
+        kernels on the same data, so the same tokens."""
         self.eval()
         if max_new_tokens <= 0:
             return input_ids
         logits, states = self.forward_with_state(input_ids)
+        graph = DecodeGraph(self, states) if use_graph and max_new_tokens > 1 else None
         for step in range(max_new_tokens):
             nxt = logits[:, -1, :] / temperature
             if top_k is not None:
@@ -136,7 +141,10 @@ class QuaternionMamba2(nn.Module):
             token = torch.multinomial(torch.softmax(nxt, dim=-1), num_samples=1)
             input_ids = torch.cat([input_ids, token], dim=1)
             if step + 1 < max_new_tokens:
-                logits, states = self._forward_with_state(token, states)
+                if graph is not None:
+                    logits = graph.step(token)
+                else:
+                    logits, states = self._forward_with_state(token, states)
         return input_ids
 
     def get_num_params(self, non_embedding: bool = True) -> int:
@@ -148,6 +156,55 @@ class QuaternionMamba2(nn.Module):
             if self.lm_head.weight is not self.embedding.weight:
                 n -= self.lm_head.weight.numel()
         return n
+
+
+class DecodeGraph:
+    """One recurrent decode step of a QuaternionMamba2 (a token per sequence
+    through every block) captured as a HIP graph, for serving loops where the
+    step's ~12 kernels per layer would otherwise each be launched from Python.
+
+    The graph reads its tokens and the per-layer states (conv tails, fp32 SSM
+    states) from static buffers and writes the new states back into them, so
+    each replay advances the sequences by one token: step(tokens) copies the
+    tokens in, replays, and returns the static logits buffer [batch, 1, vocab]
+    (valid until the next step). Built from the states a prompt's
+    forward_with_state returned (they are copied; the caller's stay as they
+    were). Capture follows torch's rules: warm-up steps on a side stream first
+    (then the states are restored), and every intermediate tensor lives in the
+    graph's memory pool. None of the library's kernels records a memset.
+    """
+
+    def __init__(self, lm: QuaternionMamba2, states, warmup: int = 2):
+        dev = lm.embedding.weight.device
+        batch = states[0][1].shape[0]
+        self.lm = lm
+        self.tokens = torch.zeros(batch, 1, dtype=torch.long, device=dev)
+        self.states = [(tail.detach().clone(), h.detach().clone()) for tail, h in states]
+        saved = [(tail.clone(), h.clone()) for tail, h in self.states]
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self._step()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = self._step()
+        for (tail, h), (t0, h0) in zip(self.states, saved):
+            tail.copy_(t0)
+            h.copy_(h0)
+
+    def _step(self) -> torch.Tensor:
+        logits, new = self.lm._forward_with_state(self.tokens, self.states)
+        for (tail, h), (nt, nh) in zip(self.states, new):
+            tail.copy_(nt)
+            h.copy_(nh)
+        return logits
+
+    def step(self, tokens: torch.Tensor) -> torch.Tensor:
+        self.tokens.copy_(tokens)
+        self.graph.replay()
+        return self.logits
 
 
 def quaternion_mamba2_small(vocab_size: int) -> QuaternionMamba2:
