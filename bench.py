@@ -303,6 +303,12 @@ def run_full(args):
         stages["B_proj GEMM mqc_gemm_nt (MFMA, this library)"] = event_time_ms(
             lambda: mqc_gemm(xa, wb, gemm_out), 5)
         del gemm_out, xa
+        # The d-sliced B/C path on the same block and input (96 d's per slice:
+        # 16 slices of two GEMMs and one chunked SSM each) against the whole
+        # projections the block uses at this size.
+        blk.bc_slice_d = 96
+        stages["block forward, B/C in slices of 96 d's"] = event_time_ms(lambda: blk(x), 3)
+        blk.bc_slice_d = None
     qln_gbs = qln_bytes(B * T, DI) / (stages["qln"] * 1e-3) / 1e9
     del delta, s, Bq, Cq
     torch.cuda.empty_cache()
@@ -325,6 +331,7 @@ def run_full(args):
     del z, q
     torch.cuda.empty_cache()
 
+    long_ctx = None if args.block_only else long_context_timing(blk)
     train = None if args.block_only else train_timings(args)
     lm = None if args.block_only else lm_timing(args)
 
@@ -373,11 +380,49 @@ def run_full(args):
             "cayley_c2_ms": round(cay_ms, 4),
             "cumprod_scan_c2_ms": round(scan_ms, 4),
         },
+        "long_context": long_ctx,
         "train_c4": train,
         "lm_c5": lm,
         "cpu_baseline": base,
     }
     print(json.dumps(result), flush=True)
+
+
+LONG_T = 262144
+
+
+def long_context_timing(blk):
+    """The benchmark's block (config-3 width, bf16) on one sequence of LONG_T
+    tokens. Whole B and C would take 2 x 206 GB; the inference forward slices
+    them (BC_WHOLE_MAX_BYTES), 8 d's per slice of 2 GiB, each slice's SSM cut
+    into time chunks."""
+    import torch
+    from mambaqc_amd import block as bm
+
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(1, LONG_T, DM, generator=g, device="cuda").to(torch.bfloat16)
+    width = bm.bc_slice_width(1, LONG_T, DI, DS, 2)
+    torch.cuda.reset_peak_memory_stats()
+    base_mem = torch.cuda.memory_allocated()
+    with torch.inference_mode():
+        blk(x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        reps = 2
+        for _ in range(reps):
+            blk(x)
+        torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    peak = torch.cuda.max_memory_allocated() - base_mem
+    log(f"long context: B1 T{LONG_T} block forward {ms:.1f} ms ({LONG_T / ms * 1e3:.0f} tokens/s), "
+        f"{width} d's per B/C slice, peak {peak / 2**30:.1f} GiB beyond the inputs")
+    del x
+    torch.cuda.empty_cache()
+    return {"workload": f"QuaternionMamba2Block forward (config-3 width, bf16), batch 1, "
+                        f"seq_len {LONG_T}, B/C projections in d-slices",
+            "ms_per_step": round(ms, 2), "tokens_per_s": round(LONG_T / ms * 1e3, 1),
+            "bc_slice_d": width, "whole_bc_bytes": 2 * LONG_T * DI * DS * 4 * 2,
+            "peak_alloc_GiB": round(peak / 2**30, 2)}
 
 
 def train_timings(args):

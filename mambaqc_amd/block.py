@@ -35,7 +35,7 @@ import torch.nn as nn
 
 from . import _native as nat
 from .kernels.quaternion_norm import QuaternionLayerNorm
-from .kernels.ssm_fused import ssm_forward_front_dl
+from .kernels.ssm_fused import ssm_forward_front_dl, ssm_forward_fused_dl, ssm_front
 from .layers.causal_conv1d import CausalConv1d, causal_conv1d_silu
 from .layers.quaternion_linear import quaternion_to_real_projection, real_to_quaternion_projection
 
@@ -115,8 +115,37 @@ def _rows_uniform(z: torch.Tensor) -> bool:
     return True
 
 
+# Inference only. The B and C projections ([batch, seq_len, d_inner, d_state, 4]
+# each, 12.9 GB together in bf16 at batch 4, seq_len 2048, d_inner 1536,
+# d_state 64) are materialised whole while both fit BC_WHOLE_MAX_BYTES. Past
+# that the forward computes them d-slice by d-slice into two reused buffers of
+# at most BC_SLICE_BYTES together and runs each slice's SSM from them, so the
+# block's memory no longer grows with batch * seq_len * d_inner * d_state (at
+# batch 1 and 262 144 tokens of the config-3 width, whole B and C would be
+# 412 GB, more than one GPU's HBM). Whole is faster where it fits: at config 3
+# the sliced form measured 18.5-18.9 ms against 16.7 ms for the GEMMs and SSM.
+BC_WHOLE_MAX_BYTES = 32 << 30
+BC_SLICE_BYTES = 2 << 30
+
+
+def bc_slice_width(batch: int, seq_len: int, d_inner: int, d_state: int, elsize: int,
+                   budget: int | None = None) -> int:
+    """d's per slice so that one slice's B and C take at most `budget` bytes
+    (None: BC_SLICE_BYTES), at least 1 and at most d_inner."""
+    if budget is None:
+        budget = BC_SLICE_BYTES
+    per_d = 2 * batch * seq_len * d_state * 4 * elsize
+    return max(1, min(d_inner, budget // max(per_d, 1)))
+
+
 class QuaternionMamba2Block(nn.Module):
-    """One Quaternion Mamba-2 block. Input and output: [batch, seq_len, d_model]."""
+    """One Quaternion Mamba-2 block. Input and output: [batch, seq_len, d_model].
+
+    bc_slice_d (attribute, not a parameter): None lets the inference forward
+    slice the B/C projections only when whole ones would exceed
+    BC_WHOLE_MAX_BYTES; an int forces slices of that many d's (inference only);
+    0 never slices.
+    """
 
     def __init__(self, d_model: int, d_state: int = 64, d_conv: int = 4,
                  expand_factor: int = 2, dt_rank: str | int = "auto", bias: bool = False):
@@ -140,6 +169,7 @@ class QuaternionMamba2Block(nn.Module):
         self.gate_proj = nn.Linear(D, D, bias=False)
         self.norm = QuaternionLayerNorm(D, eps=1e-5)
         self.out_proj = quaternion_to_real_projection(D, d_model, bias=bias)
+        self.bc_slice_d: int | None = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         xz = self.in_proj(x)
@@ -182,13 +212,83 @@ class QuaternionMamba2Block(nn.Module):
                      return_state: bool = False):
         """x: [batch, seq_len, d_inner] (real) -> y: [batch, seq_len, d_inner, 4]."""
         b, t, D = x.shape
+        width = self._bc_slice_width(x)
         dt_raw = self.dt_proj(x)
+        g_raw = self.gate_proj(x)
+        if width:
+            return self._ssm_forward_sliced(x, dt_raw, g_raw, width, h0, return_state)
         Bq = self.B_proj(x).view(b, t, D, self.d_state, 4)
         Cq = self.C_proj(x).view(b, t, D, self.d_state, 4)
-        g_raw = self.gate_proj(x)
         return ssm_forward_front_dl(dt_raw, g_raw, x, Bq, Cq, self.Lambda_alpha,
                                     self.Lambda_imag, self.D, eps=1e-6, h0=h0,
                                     return_state=return_state)
+
+    def _gemm_dtype(self, x: torch.Tensor) -> torch.dtype:
+        if torch.is_autocast_enabled(x.device.type):
+            return torch.get_autocast_dtype(x.device.type)
+        return x.dtype
+
+    def _bc_slice_width(self, x: torch.Tensor) -> int:
+        """d's per B/C slice for this input, 0 for whole projections."""
+        forced = self.bc_slice_d
+        if forced == 0:
+            return 0
+        recording = torch.is_grad_enabled() and (x.requires_grad or any(
+            p.requires_grad for p in self.parameters()))
+        if forced is not None:
+            if forced < 0:
+                raise ValueError(f"bc_slice_d must be >= 0 or None, got {forced}")
+            if recording:
+                raise ValueError("bc_slice_d: sliced B/C projections are inference-only "
+                                 "(the backward needs B and C whole)")
+            return min(int(forced), self.d_inner)
+        if recording or self.B_proj.bias is not None or self.C_proj.bias is not None:
+            return 0
+        b, t, D = x.shape
+        el = torch.empty(0, dtype=self._gemm_dtype(x)).element_size()
+        if 2 * b * t * D * self.d_state * 4 * el <= BC_WHOLE_MAX_BYTES:
+            return 0
+        return bc_slice_width(b, t, D, self.d_state, el)
+
+    def _ssm_forward_sliced(self, x, dt_raw, g_raw, width, h0, return_state):
+        """The SSM with B and C computed `width` d's at a time into two reused
+        buffers: per slice, the two projection GEMMs (rows of the weights as
+        stored) and the SSM over that slice's d's, from that slice's h0.
+        Each (b, d) state depends only on its own d's B, C, delta and s, so
+        the slices are independent."""
+        if self.B_proj.bias is not None or self.C_proj.bias is not None:
+            raise ValueError("sliced B/C projections take bias-free B_proj and C_proj")
+        b, t, D = x.shape
+        S = self.d_state
+        delta, s = ssm_front(dt_raw, g_raw, x)
+        dtype = self._gemm_dtype(x)
+        x2 = x.reshape(b * t, D).to(dtype)
+        wb, wc = self.B_proj.weight.detach(), self.C_proj.weight.detach()
+        # fp32 forms of the SSM parameters, converted once (cached) and sliced.
+        la, li, dv = (nat.param_f32(p) for p in (self.Lambda_alpha, self.Lambda_imag, self.D))
+        per = b * t * width * S * 4
+        buf = torch.empty(2, per, device=x.device, dtype=dtype)
+        y = torch.empty(b, t, D, 4, device=x.device, dtype=dtype)
+        h_last = (torch.empty(b, D, S, 4, device=x.device, dtype=torch.float32)
+                  if return_state else None)
+        with torch.autocast(x.device.type, enabled=False):
+            for d0 in range(0, D, width):
+                n = min(width, D - d0)
+                r0, r1 = d0 * S * 4, (d0 + n) * S * 4
+                bs = buf[0, : b * t * n * S * 4].view(b * t, n * S * 4)
+                cs = buf[1, : b * t * n * S * 4].view(b * t, n * S * 4)
+                torch.mm(x2, wb[r0:r1].to(dtype).t(), out=bs)
+                torch.mm(x2, wc[r0:r1].to(dtype).t(), out=cs)
+                out = ssm_forward_fused_dl(
+                    delta[:, :, d0:d0 + n], s[:, :, d0:d0 + n], bs.view(b, t, n, S, 4),
+                    cs.view(b, t, n, S, 4), la[d0:d0 + n], li[d0:d0 + n], dv[d0:d0 + n],
+                    eps=1e-6,
+                    h0=None if h0 is None else h0[:, d0:d0 + n], return_state=return_state)
+                if return_state:
+                    out, h_slice = out
+                    h_last[:, d0:d0 + n] = h_slice
+                y[:, :, d0:d0 + n] = out
+        return (y, h_last) if return_state else y
 
     def extra_repr(self) -> str:
         return (f"d_model={self.d_model}, d_state={self.d_state}, d_inner={self.d_inner}, "

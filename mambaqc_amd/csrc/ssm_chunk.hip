@@ -42,14 +42,17 @@ int scratch_ptr(void** out) {
 // delta, s and B (the carry launch) and a short prefix launch.
 constexpr int64_t kMinChunk = 64;
 // The whole walk keeps the machine busy from this many states up (config 3:
-// 4 x 1536 x 64); fewer get more chunks, up to kMaxChunks. Measured on MI355X
-// (bf16, T 2048, whole walk -> best chunking, ms): B1 d_inner 1536 S64
-// 0.964 -> 0.824 (4 chunks), B1 d768 S64 0.698 -> 0.426 (8), B1 T4096 d1536
-// S64 1.82 -> 1.64 (4); B2 d1536 S64 1.25 and B4 d1536 S16 0.85 only got
-// slower (1.37, 0.90 with 2 chunks): the carry launch re-reads B, 25-38 % more
-// bytes, which only pays where the whole walk is far from the bandwidth.
+// 4 x 1536 x 64); fewer get chunks until states x chunks reaches it, at most
+// kMaxChunks. Measured on MI355X (bf16, whole walk -> best chunking, ms):
+// T 2048: B1 d_inner 1536 S64 0.964 -> 0.824 (4 chunks), B1 d768 S64
+// 0.698 -> 0.426 (8), B1 T4096 d1536 S64 1.82 -> 1.64 (4); B2 d1536 S64 1.25
+// and B4 d1536 S16 0.85 only got slower (1.37, 0.90 with 2 chunks): the carry
+// launch re-reads B, 25-38 % more bytes, which only pays where the whole walk
+// is far from the bandwidth. Long walks of few states (the d-slices of a long
+// sequence): B1 T262144 d8 S64 88.4 -> 0.65 (512 chunks; 17.3 with 8),
+// B1 T65536 d32 S64 22.8 -> 0.61 (256), B1 T16384 d96 S64 5.70 -> 0.47 (64).
 constexpr int64_t kBusyStates = 393216;
-constexpr int64_t kMaxChunks = 8;
+constexpr int64_t kMaxChunks = 1024;
 // Below 32 states per (b, d) the whole walk already packs one state per lane
 // into short groups; chunk those only when the states are fewer than this.
 constexpr int64_t kFewStates = 49152;

@@ -160,7 +160,8 @@ def test_chunk_policy_and_workspace_without_gpu():
     """The library's chunk choice for the inference walk: none where
     batch * d_inner * d_state states come near filling the GPU (config 3's
     393 216 states, or half of them) or the walk is short; chunks of at least
-    64 steps, at most 8 of them, more for fewer states.
+    64 steps, more for fewer states (states x chunks about 393 216), at most
+    1024 of them.
     The workspace size formula, and the chunked entry point's validation."""
     from mambaqc_amd.kernels.ssm_fused import chunk_len_for
 
@@ -175,6 +176,11 @@ def test_chunk_policy_and_workspace_without_gpu():
     assert chunk_len_for(4, 2048, 1536, 16, bf) == 2048
     L8 = chunk_len_for(1, 2048, 768, 64, bf)
     assert 64 <= L8 < L and -(-2048 // L8) <= 8
+    # Long walks of few states: chunks until states x chunks reaches 393 216.
+    assert chunk_len_for(1, 262144, 8, 64, bf) == -(-262144 // 768)
+    assert chunk_len_for(1, 16384, 96, 64, bf) == 256
+    assert chunk_len_for(1, 1 << 20, 1, 64, bf) == 1024  # 1024 chunks at most
+    assert chunk_len_for(1, 2048, 8, 64, bf) == 64        # chunks of 64 steps at least
     lib = nat.load()
     assert lib.mqc_ssm_chunked_workspace_bytes(1, 2048, 1536, 64, 512) == 24 * 3 * 1536 * 64
     assert lib.mqc_ssm_chunked_workspace_bytes(2, 10, 3, 4, 10) == 0
@@ -338,3 +344,30 @@ def test_build_rejects_kernels_that_spill():
     ])
     assert B._spilling_kernels(log) == ["_Z4slowv (116 bytes/lane)"]
     assert B.RESOURCE_REMARKS == "-Rpass-analysis=kernel-resource-usage"
+
+
+def test_bc_slice_rule():
+    """The sliced B/C rule without a GPU: widths from the byte budget, whole
+    projections below the bound, and forced slicing refused when autograd
+    records (the backward needs B and C whole)."""
+    import mambaqc_amd
+    from mambaqc_amd import block as bm
+    assert bm.bc_slice_width(1, 262144, 1536, 64, 2) == 8
+    assert bm.bc_slice_width(4, 2048, 1536, 64, 2, budget=1) == 1
+    assert bm.bc_slice_width(1, 4, 16, 4, 4, budget=1 << 40) == 16
+    blk = mambaqc_amd.QuaternionMamba2Block(32, d_state=4)
+    x = torch.zeros(2, 8, 64)
+    with torch.no_grad():
+        assert blk._bc_slice_width(x) == 0
+        blk.bc_slice_d = 5
+        assert blk._bc_slice_width(x) == 5
+        blk.bc_slice_d = 1000
+        assert blk._bc_slice_width(x) == 64
+        blk.bc_slice_d = -1
+        with pytest.raises(ValueError):
+            blk._bc_slice_width(x)
+    blk.bc_slice_d = 5
+    with pytest.raises(ValueError, match="inference-only"):
+        blk._bc_slice_width(x)
+    blk.bc_slice_d = None
+    assert blk._bc_slice_width(x) == 0
