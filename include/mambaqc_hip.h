@@ -122,8 +122,9 @@ int mqc_ssm_fused_fwd(const void* delta, const void* s, const void* B, const voi
 
 /* Chunk length mqc_ssm_fused_fwd_chunked would be given by a caller that lets
  * the library choose: seq_len (one chunk, the whole walk) when batch * d_inner
- * * d_state states keep the GPU busy on their own, shorter chunks (at least 64
- * steps, at most 8 chunks) when they do not. Negative: an MQC_E_* code. */
+ * * d_state states keep the GPU busy on their own, shorter chunks when they
+ * do not: about 393216 / states chunks, each at least 64 steps, at most 1024
+ * chunks. Negative: an MQC_E_* code. */
 int64_t mqc_ssm_chunk_len_auto(int64_t batch, int64_t seq_len, int64_t d_inner,
                                int64_t d_state, int dtype);
 

@@ -6,6 +6,8 @@ Drop-in for the reference package's hot path (polux06/mambaqc):
                         ssm_step_fused, ssm_forward_fused, quaternion_layer_norm_fused
   mambaqc_amd.layers    QuaternionLinear, QuaternionLayerNorm, CausalConv1d
   mambaqc_amd           QuaternionMamba2Block, QuaternionMamba2 (+ presets)
+  torch.ops.mambaqc.*   the same kernels as registered torch operators with fake
+                        kernels and autograd formulas (mambaqc_amd.ops)
 All compute of the quaternion path runs in libmambaqc_hip.so (hand-written
 HIP, C ABI in include/mambaqc_hip.h); there is no CPU fallback.
 """
@@ -18,6 +20,7 @@ from .lm import (
     quaternion_mamba2_large,
     quaternion_mamba2_small,
 )
+from . import ops  # registers torch.ops.mambaqc.*
 
 __all__ = [
     "QuaternionMamba2",

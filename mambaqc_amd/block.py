@@ -73,16 +73,21 @@ class _OutGateFunction(torch.autograd.Function):
     def backward(ctx, dout):
         zc, yc = ctx.saved_tensors
         zs, rows, d, zshape, t_x, t_z, t_y = ctx.meta
-        dout = nat.aligned16(dout.to(yc.dtype))
-        zcols = zshape[-1]
-        dz = torch.empty(zshape, device=yc.device, dtype=yc.dtype)
-        dy = torch.empty_like(yc)
-        # zc may have been narrowed to the first d columns: its gradient beyond
-        # d is zero either way.
-        nat.call("mqc_out_gate_bwd", yc, dout.data_ptr(), zc.data_ptr(), zs, yc.data_ptr(),
-                 dz.data_ptr(), dy.data_ptr(), rows, d, zcols, nat.dtype_code(yc),
-                 nat.stream_of(yc))
+        dout, dz, dy = _out_gate_backward(zc, zs, yc, rows, d, zshape, dout)
         return dout.to(t_x), dz.to(t_z), dy.to(t_y)
+
+
+def _out_gate_backward(zc, zs, yc, rows, d, zshape, dout):
+    """(dx, dz [zshape], dy_real) in the operands' dtype from the forward's
+    operands (_gate_operands). zc may have been narrowed to the first d
+    columns: dz beyond d is zero either way."""
+    dout = nat.aligned16(dout.to(yc.dtype))
+    dz = torch.empty(zshape, device=yc.device, dtype=yc.dtype)
+    dy = torch.empty_like(yc)
+    nat.call("mqc_out_gate_bwd", yc, dout.data_ptr(), zc.data_ptr(), zs, yc.data_ptr(),
+             dz.data_ptr(), dy.data_ptr(), rows, d, zshape[-1], nat.dtype_code(yc),
+             nat.stream_of(yc))
+    return dout, dz, dy
 
 
 def out_gate(x: torch.Tensor, z: torch.Tensor, y_real: torch.Tensor) -> torch.Tensor:

@@ -34,6 +34,8 @@
 //     about 1 ms this way).
 // Rows of X past M are clamped onto row M - 1 for the loads and never stored,
 // so M is free; N must be a multiple of 256 and K of 64.
+#include <atomic>
+
 #include "common.hpp"
 
 namespace mqc {
@@ -199,6 +201,11 @@ __global__ __launch_bounds__(kGThreads) void gemm_nt_bf16_kernel(const __bf16* _
 
 using namespace mqc;
 
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<bool> g_lds_attr_set[kMaxDevices];
+}  // namespace
+
 extern "C" {
 
 int mqc_gemm_nt(const void* X, const void* W, void* C, int64_t M, int64_t N, int64_t K, int dtype,
@@ -214,12 +221,17 @@ int mqc_gemm_nt(const void* X, const void* W, void* C, int64_t M, int64_t N, int
   if (M > (1LL << 30) || N > (1LL << 30) || K > (1LL << 20)) return MQC_E_LIMIT;
   const int64_t tiles = (M + kGT - 1) / kGT * (N / kGT);
   if (tiles > 0x7fffffffLL) return MQC_E_LIMIT;
-  static bool attr_set = false;  // idempotent; a race only repeats the call
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute((const void*)gemm_nt_bf16_kernel,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  // The LDS limit is a per-device attribute of the kernel: set once on each
+  // device (idempotent, so two threads racing only repeat the call).
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return MQC_E_LIMIT;
+  if (!g_lds_attr_set[dev].load(std::memory_order_acquire)) {
+    e = hipFuncSetAttribute((const void*)gemm_nt_bf16_kernel,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return (int)e;
-    attr_set = true;
+    g_lds_attr_set[dev].store(true, std::memory_order_release);
   }
   hipLaunchKernelGGL(gemm_nt_bf16_kernel, dim3((unsigned)tiles), dim3(kGThreads), kLdsBytes,
                      (hipStream_t)stream, (const __bf16*)X, (const __bf16*)W, (__bf16*)C, (int)M,

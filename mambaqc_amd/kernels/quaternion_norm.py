@@ -44,16 +44,21 @@ class _QLNFunction(torch.autograd.Function):
     def backward(ctx, dout):
         qc, g, mean, rstd = ctx.saved_tensors
         eps, t_gamma, t_beta = ctx.meta
-        B, T, D, _ = qc.shape
-        dout = nat.aligned16(dout.to(qc.dtype))
-        dq = torch.empty_like(qc)
-        ne = torch.empty(B * T, D, device=qc.device, dtype=torch.float32)
-        nat.call("mqc_qln_bwd", qc, qc.data_ptr(), dout.data_ptr(), g.data_ptr(),
-                 mean.data_ptr(), rstd.data_ptr(), dq.data_ptr(), ne.data_ptr(), B * T, D,
-                 float(eps), nat.dtype_code(qc), nat.stream_of(qc))
-        dgamma = ne.sum(0)
-        dbeta = dout.float().reshape(B * T, D, 4).sum(0)
+        dq, dgamma, dbeta = _qln_backward(qc, g, mean, rstd, dout, eps)
         return dq, dgamma.to(t_gamma), dbeta.to(t_beta), None
+
+
+def _qln_backward(qc, g, mean, rstd, dout, eps):
+    """(dq in q's dtype, dgamma [D] and dbeta [D, 4] in fp32) from the forward's
+    operands (q in the kernel's form, gamma fp32) and statistics."""
+    B, T, D, _ = qc.shape
+    dout = nat.aligned16(dout.to(qc.dtype))
+    dq = torch.empty_like(qc)
+    ne = torch.empty(B * T, D, device=qc.device, dtype=torch.float32)
+    nat.call("mqc_qln_bwd", qc, qc.data_ptr(), dout.data_ptr(), g.data_ptr(),
+             mean.data_ptr(), rstd.data_ptr(), dq.data_ptr(), ne.data_ptr(), B * T, D,
+             float(eps), nat.dtype_code(qc), nat.stream_of(qc))
+    return dq, ne.sum(0), dout.float().reshape(B * T, D, 4).sum(0)
 
 
 def quaternion_layer_norm_fused(q: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor,

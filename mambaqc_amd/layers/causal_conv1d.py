@@ -71,19 +71,26 @@ class _ConvSiLU(torch.autograd.Function):
     def backward(ctx, gout):
         xv, w, b = ctx.saved_tensors
         xs, wshape, t_w, t_b = ctx.meta
-        B, T, C = xv.shape
-        K = w.shape[1]
-        gout = nat.aligned16(gout.to(xv.dtype))
-        R = nat.load().mqc_conv_run_length()
-        rows = B * ((T + R - 1) // R)
-        dx = torch.empty(B, T, C, device=xv.device, dtype=xv.dtype)
-        dw = torch.empty(rows, C, K, device=xv.device, dtype=torch.float32)
-        db = torch.empty(rows, C, device=xv.device, dtype=torch.float32)
-        nat.call("mqc_causal_conv_silu_bwd", xv, xv.data_ptr(), xs, w.data_ptr(), nat.ptr(b),
-                 gout.data_ptr(), dx.data_ptr(), C, dw.data_ptr(), db.data_ptr(), B, T, C, K,
-                 nat.dtype_code(xv), nat.stream_of(xv))
-        return (dx, dw.sum(0).reshape(wshape).to(t_w),
-                None if t_b is None else db.sum(0).to(t_b))
+        dx, dw, db = _conv_silu_backward(xv, xs, w, b, gout)
+        return (dx, dw.reshape(wshape).to(t_w), None if t_b is None else db.to(t_b))
+
+
+def _conv_silu_backward(xv, xs, w, b, gout):
+    """(dx [B, T, C] in x's dtype, dweight [C, K] and dbias [C] in fp32) from the
+    forward's operands: x as a row view with row stride xs, weight [C, K] and
+    bias (or None) in fp32."""
+    B, T, C = xv.shape
+    K = w.shape[1]
+    gout = nat.aligned16(gout.to(xv.dtype))
+    R = nat.load().mqc_conv_run_length()
+    rows = B * ((T + R - 1) // R)
+    dx = torch.empty(B, T, C, device=xv.device, dtype=xv.dtype)
+    dw = torch.empty(rows, C, K, device=xv.device, dtype=torch.float32)
+    db = torch.empty(rows, C, device=xv.device, dtype=torch.float32)
+    nat.call("mqc_causal_conv_silu_bwd", xv, xv.data_ptr(), xs, w.data_ptr(), nat.ptr(b),
+             gout.data_ptr(), dx.data_ptr(), C, dw.data_ptr(), db.data_ptr(), B, T, C, K,
+             nat.dtype_code(xv), nat.stream_of(xv))
+    return dx, dw.sum(0), db.sum(0)
 
 
 def causal_conv1d_silu(x: torch.Tensor, weight: torch.Tensor,

@@ -371,3 +371,46 @@ def test_bc_slice_rule():
         blk._bc_slice_width(x)
     blk.bc_slice_d = None
     assert blk._bc_slice_width(x) == 0
+
+
+def test_torch_ops_registered_with_fake_kernels():
+    """Every kernel is a registered torch.ops.mambaqc op whose fake kernel gives
+    the output shapes and dtypes on the meta device (no GPU, nothing runs);
+    a CPU tensor reaching a real kernel raises instead of falling back."""
+    from mambaqc_amd import ops
+
+    mm = torch.ops.mambaqc
+    for name in ops.OPS:
+        assert hasattr(mm, name), name
+
+    def m(*shape, dt=torch.float32):
+        return torch.empty(*shape, device="meta", dtype=dt)
+
+    bf = torch.bfloat16
+    sh = lambda ts: [(tuple(t.shape), t.dtype) for t in (ts if isinstance(ts, (tuple, list)) else [ts])]
+    assert sh(mm.quaternion_multiply(m(3, 5, 4), m(3, 5, 4))) == [((3, 5, 4), torch.float32)]
+    assert sh(mm.quaternion_norm(m(3, 5, 4, dt=bf))) == [((3, 5), bf)]
+    assert sh(mm.cumprod_scan(m(2, 7, 3, 2, 4))) == [((2, 7, 3, 2, 4), torch.float32)]
+    assert sh(mm.ssm_forward_q(m(2, 7, 3, 2, 4), m(2, 7, 3, 2, 4), m(2, 7, 3, 4),
+                               m(2, 7, 3, 2, 4), m(2, 7, 3))) == [((2, 7, 3, 4), torch.float32)]
+    assert sh(mm.ssm_step_q(m(2, 3, 5, 4), m(2, 3, 5, 4), m(2, 3, 4), m(2, 3, 5, 4), m(2, 3),
+                            m(2, 3, 5, 4))) == [((2, 3, 5, 4), torch.float32), ((2, 3, 4), torch.float32)]
+    dl = (m(2, 17, 3, dt=bf), m(2, 17, 3, dt=bf), m(2, 17, 3, 4, 4, dt=bf), m(2, 17, 3, 4, 4, dt=bf),
+          m(3, 4), m(3, 4, 3), m(3))
+    assert sh(mm.ssm_forward_dl(*dl)) == [((2, 17, 3, 4), bf), ((2, 3, 4, 4), torch.float32)]
+    # 16-bit storage: a checkpoint every 8 steps.
+    assert sh(mm.ssm_forward_dl_train(*dl)) == [((2, 17, 3, 4), bf), ((2, 3, 4, 4), torch.float32),
+                                                ((2, 3, 3, 4, 4), torch.float32)]
+    g = mm.ssm_backward_dl(*dl, None, m(2, 3, 3, 4, 4), m(2, 17, 3, 4, dt=bf), None)
+    assert sh(g) == [((2, 17, 3), torch.float32)] * 2 + [((2, 17, 3, 4, 4), bf)] * 2 + [
+        ((3, 4), torch.float32), ((3, 4, 3), torch.float32), ((3,), torch.float32),
+        ((0,), torch.float32)]
+    assert sh(mm.ssm_front(m(2, 5, 3, dt=bf), m(2, 5, 3, dt=bf), m(2, 5, 3))) == [((2, 5, 3), torch.float32)] * 2
+    assert sh(mm.quaternion_layer_norm(m(2, 5, 3, 4, dt=bf), m(3), m(3, 4))) == [
+        ((2, 5, 3, 4), bf), ((2, 5), torch.float32), ((2, 5), torch.float32)]
+    assert sh(mm.causal_conv1d_silu(m(2, 5, 3, dt=bf), m(3, 1, 4), m(3))) == [((2, 5, 3), bf)]
+    assert sh(mm.causal_conv1d_silu_backward(m(2, 5, 3, dt=bf), m(3, 1, 4), None, m(2, 5, 3, dt=bf))) == [
+        ((2, 5, 3), bf), ((3, 4), torch.float32), ((3,), torch.float32)]
+    assert sh(mm.out_gate(m(2, 5, 8), m(2, 5, 16, dt=bf), m(2, 5, 8, dt=bf))) == [((2, 5, 8), torch.float32)]
+    with pytest.raises(RuntimeError):
+        mm.quaternion_multiply(torch.zeros(2, 4), torch.zeros(2, 4))
