@@ -187,7 +187,14 @@ def param_f32(t: torch.Tensor) -> torch.Tensor:
 
 
 def call(name: str, device_tensor: torch.Tensor, *args) -> None:
-    lib = load()
-    with torch.cuda.device(device_tensor.device):
-        status = getattr(lib, name)(*args)
+    """Call entry point `name` with the tensor's device current (the library
+    launches on the device that is current; the stream argument must belong to
+    it). The device switch is skipped when it is current already."""
+    fn = getattr(load(), name)
+    idx = device_tensor.device.index
+    if idx is None or idx == torch.cuda.current_device():
+        status = fn(*args)
+    else:
+        with torch.cuda.device(idx):
+            status = fn(*args)
     check(status, name)
