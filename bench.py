@@ -1,7 +1,7 @@
 """Benchmark: QuaternionMamba2Block forward on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
-                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|decode|decode_graph|train|copy]
+                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|decode|decode_graph|block_long|train|copy]
                     [--preset small|base|large]
 
 Workload (BASELINE configs[2]/[3] shape): one QuaternionMamba2Block forward,
@@ -610,6 +610,15 @@ def run_kernel_loop(args):
                     graph = DecodeGraph(lm, states)
                 fn = lambda: graph.step(tok)
             nbytes = sum(p.numel() * p.element_size() for p in lm.parameters())
+        elif args.mode == "block_long":
+            # The long-context line: the benchmark's block on one sequence of
+            # LONG_T tokens, B/C projections in d-slices.
+            torch.manual_seed(0)
+            with torch.inference_mode(False):
+                blk = make_block(torch.bfloat16)
+            x = torch.randn(1, LONG_T, DM, generator=g, device="cuda").to(torch.bfloat16)
+            fn = lambda: blk(x)
+            nbytes = 0
         elif args.mode == "train":
             # Config 4: block forward + backward under fp16 autocast, loss
             # scaled as in train_timings (kernel traces of the training step).
