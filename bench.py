@@ -1,7 +1,7 @@
 """Benchmark: QuaternionMamba2Block forward on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
-                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|decode|decode_graph|block_long|train|copy]
+                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_train|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|decode|decode_graph|block_long|train|copy]
                     [--preset small|base|large]
 
 Workload (BASELINE configs[2]/[3] shape): one QuaternionMamba2Block forward,
@@ -562,6 +562,19 @@ def run_kernel_loop(args):
             L = T if args.mode == "ssm_b1_whole" else None
             fn = lambda: K.ssm_forward_fused_dl(delta, s, Bq, Cq, la, li, Dv, chunk_len=L)
             nbytes = ssm_bytes(bb, T, DI, DS)
+        elif args.mode == "ssm_train":
+            # The SSM's training forward (walk + fp32 state checkpoints) at config 3.
+            from mambaqc_amd.kernels.ssm_fused import ssm_fused_dl_train_forward
+            bf = torch.bfloat16
+            delta = torch.nn.functional.softplus(torch.randn(B, T, DI, generator=g, device="cuda") - 2).to(bf)
+            s = torch.randn(B, T, DI, generator=g, device="cuda").to(bf)
+            Bq = torch.randn(B, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
+            Cq = torch.randn(B, T, DI, DS, 4, generator=g, device="cuda", dtype=bf) * 0.02
+            la = torch.randn(DI, DS, generator=g, device="cuda") * 0.5 + 1
+            li = torch.randn(DI, DS, 3, generator=g, device="cuda") * 0.1
+            Dv = torch.ones(DI, device="cuda")
+            fn = lambda: ssm_fused_dl_train_forward(delta, s, Bq, Cq, la, li, Dv)
+            nbytes = ssm_bytes(B, T, DI, DS) + B * ((T + 7) // 8) * DI * DS * 16
         elif args.mode == "ssm_bwd":
             from mambaqc_amd.kernels.ssm_fused import (ssm_fused_dl_backward,
                                                        ssm_fused_dl_train_forward)
