@@ -172,6 +172,11 @@ class DecodeGraph:
     were). Capture follows torch's rules: warm-up steps on a side stream first
     (then the states are restored), and every intermediate tensor lives in the
     graph's memory pool. None of the library's kernels records a memset.
+
+    The graph holds the device addresses it was captured with, including the
+    fp32 copies of 16-bit parameters that the kernels read: build it once the
+    weights are final, and build a new one after any weight update or
+    .to()/.load_state_dict() on the model.
     """
 
     def __init__(self, lm: QuaternionMamba2, states, warmup: int = 2):
