@@ -142,6 +142,13 @@ def require_device(name: str, *tensors: torch.Tensor) -> None:
             raise RuntimeError(f"mambaqc_amd.{name}: tensors on different devices ({dev}, {t.device})")
 
 
+def compiling() -> bool:
+    """True while torch.compile traces: the Python API then calls the
+    registered torch.ops.mambaqc.* operators (traceable through their fake
+    kernels) instead of ctypes."""
+    return torch.compiler.is_compiling()
+
+
 def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 

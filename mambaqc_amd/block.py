@@ -100,6 +100,8 @@ def out_gate(x: torch.Tensor, z: torch.Tensor, y_real: torch.Tensor) -> torch.Te
     d = x.shape[-1]
     assert y_real.shape == x.shape, f"y_real {tuple(y_real.shape)} vs x {tuple(x.shape)}"
     assert z.shape[:-1] == x.shape[:-1] and z.shape[-1] >= d
+    if nat.compiling():
+        return torch.ops.mambaqc.out_gate(x, z, y_real)
     nat.require_device("out_gate", x, z, y_real)
     if torch.is_grad_enabled() and any(t.requires_grad for t in (x, z, y_real)):
         return _OutGateFunction.apply(x, z, y_real)
@@ -250,7 +252,7 @@ class QuaternionMamba2Block(nn.Module):
         if recording or self.B_proj.bias is not None or self.C_proj.bias is not None:
             return 0
         b, t, D = x.shape
-        el = torch.empty(0, dtype=self._gemm_dtype(x)).element_size()
+        el = 4 if self._gemm_dtype(x) == torch.float32 else 2
         if 2 * b * t * D * self.d_state * 4 * el <= BC_WHOLE_MAX_BYTES:
             return 0
         return bc_slice_width(b, t, D, self.d_state, el)

@@ -73,6 +73,9 @@ def quaternion_layer_norm_fused(q: torch.Tensor, gamma: torch.Tensor, beta: torc
     assert q.ndim == 4, f"Expected [B, T, D, 4], got {q.shape}"
     assert gamma.shape == (q.shape[2],), f"gamma shape mismatch: {gamma.shape}"
     assert beta.shape == (q.shape[2], 4), f"beta shape mismatch: {beta.shape}"
+    if nat.compiling():
+        out, mean, rstd = torch.ops.mambaqc.quaternion_layer_norm(q, gamma, beta, eps)
+        return (out, mean, rstd) if return_stats else out
     nat.require_device("quaternion_layer_norm_fused", q, gamma, beta)
     if (torch.is_grad_enabled() and not return_stats
             and any(t.requires_grad for t in (q, gamma, beta))):

@@ -280,6 +280,9 @@ def ssm_forward_fused_dl(delta: torch.Tensor, s: torch.Tensor, B: torch.Tensor,
     forces that length, >= seq_len meaning the whole walk).
     """
     inputs = (delta, s, B, C, lambda_alpha, lambda_imag, D) + ((h0,) if h0 is not None else ())
+    if nat.compiling():
+        return _dl_ops(delta, s, B, C, lambda_alpha, lambda_imag, D, h0, eps, return_state,
+                       chunk_len, inputs)
     if torch.is_grad_enabled() and any(t.requires_grad for t in inputs):
         _require_trainable_state(B)
         y, h_last = _SsmFusedDL.apply(delta, s, B, C, lambda_alpha, lambda_imag, D, h0, eps)
@@ -287,6 +290,20 @@ def ssm_forward_fused_dl(delta: torch.Tensor, s: torch.Tensor, B: torch.Tensor,
     _dl_check(delta, s, B, C, lambda_alpha, lambda_imag, D, h0)
     ops = _dl_operands(delta, s, B, C, lambda_alpha, lambda_imag, D, h0)
     return _launch_dl_inference(*ops, eps, return_state, chunk_len)
+
+
+def _dl_ops(delta, s, B, C, lambda_alpha, lambda_imag, D, h0, eps, return_state, chunk_len,
+            inputs):
+    """The delta-lambda SSM through the registered operators (torch.compile):
+    the training walk when autograd records, else the inference walk."""
+    if torch.is_grad_enabled() and any(t.requires_grad for t in inputs):
+        _require_trainable_state(B)
+        y, h_last, _ = torch.ops.mambaqc.ssm_forward_dl_train(delta, s, B, C, lambda_alpha,
+                                                              lambda_imag, D, h0, eps)
+    else:
+        y, h_last = torch.ops.mambaqc.ssm_forward_dl(delta, s, B, C, lambda_alpha, lambda_imag,
+                                                     D, h0, eps, chunk_len)
+    return (y, h_last) if return_state else y
 
 
 def _front_operands(dt_raw, g_raw, x):
@@ -313,6 +330,8 @@ def ssm_front(dt_raw: torch.Tensor, g_raw: torch.Tensor, x: torch.Tensor):
     mambaqc/models/quaternion_mamba2_block.py:183,197-198. The three tensors have
     one shape; the results come in their promoted dtype (fp32 arithmetic).
     """
+    if nat.compiling():
+        return torch.ops.mambaqc.ssm_front(dt_raw, g_raw, x)
     return _front_forward(*_front_operands(dt_raw, g_raw, x))
 
 
@@ -365,6 +384,12 @@ def ssm_forward_front_dl(dt_raw: torch.Tensor, g_raw: torch.Tensor, x: torch.Ten
     Differentiable in every tensor argument when autograd is recording."""
     inputs = (dt_raw, g_raw, x, B, C, lambda_alpha, lambda_imag, D) + (
         (h0,) if h0 is not None else ())
+    if nat.compiling():
+        # Front and SSM as two traced operators (the eager path keeps them in
+        # one autograd node so that d_delta reaches the front in fp32).
+        delta, s = torch.ops.mambaqc.ssm_front(dt_raw, g_raw, x)
+        return _dl_ops(delta, s, B, C, lambda_alpha, lambda_imag, D, h0, eps, return_state,
+                       None, inputs)
     if torch.is_grad_enabled() and any(t.requires_grad for t in inputs):
         _require_trainable_state(B)
         y, h_last = _SsmFrontFusedDL.apply(dt_raw, g_raw, x, B, C, lambda_alpha, lambda_imag,

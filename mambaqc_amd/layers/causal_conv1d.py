@@ -100,5 +100,7 @@ def causal_conv1d_silu(x: torch.Tensor, weight: torch.Tensor,
     Conv1d's), bias [channels] or None -> dense [batch, seq_len, channels].
     Differentiable when autograd is recording."""
     assert x.ndim == 3 and weight.shape[0] == x.shape[-1]
+    if nat.compiling():
+        return torch.ops.mambaqc.causal_conv1d_silu(x, weight, bias)
     nat.require_device("causal_conv1d_silu", x, weight)
     return _ConvSiLU.apply(x, weight, bias)

@@ -112,7 +112,8 @@ def wide_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     n, k = weight.shape
     rows = x.numel() // k if k else 0
     if (n * k * weight.element_size() <= WIDE_LINEAR_CHUNK_BYTES or rows < WIDE_LINEAR_MIN_ROWS
-            or not x.is_cuda or not weight.is_cuda):
+            or not x.is_cuda or not weight.is_cuda or torch.compiler.is_compiling()):
+        # (Under torch.compile the product is left to the compiler as one GEMM.)
         return F.linear(x, weight)
     dtype = None
     if torch.is_autocast_enabled(x.device.type):

@@ -195,3 +195,30 @@ def test_compiled_pipeline_equals_eager():
         fn = torch.compile(pipeline, backend="aot_eager", fullgraph=True)
         got = fn(xa, dt, gr, Bq, Cq, x, z, yproj)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype,rtol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_block_compiles_fullgraph(dtype, rtol):
+    """torch.compile(block, fullgraph=True) traces the whole block: the kernels
+    enter the graph as torch.ops.mambaqc.* operators. Forward and gradients
+    against the eager block (aot_eager runs the traced graph as is)."""
+    torch.manual_seed(3)
+    blk = mambaqc_amd.QuaternionMamba2Block(32, d_state=8).to(DEV, dtype)
+    x = torch.randn(2, 40, 32, generator=_g(4), device=DEV).to(dtype)
+    compiled = torch.compile(blk, backend="aot_eager", fullgraph=True)
+    with torch.no_grad():
+        want = blk(x)
+        got = compiled(x)
+    from conftest import assert_close
+    assert_close(got, want, rtol, "compiled block forward (no grad)")
+    xe = x.clone().requires_grad_()
+    xc = x.clone().requires_grad_()
+    gy = torch.randn(want.shape, generator=_g(5), device=DEV).to(dtype)
+    ye = blk(xe)
+    ge = torch.autograd.grad(ye, [xe] + list(blk.parameters()), gy)
+    yc = compiled(xc)
+    gc = torch.autograd.grad(yc, [xc] + list(blk.parameters()), gy)
+    assert_close(yc, ye, rtol, "compiled block forward (training)")
+    names = ["x"] + [n for n, _ in blk.named_parameters()]
+    for n, a, b in zip(names, gc, ge):
+        assert_close(a, b, max(rtol, 1e-4), f"compiled block grad {n}")
