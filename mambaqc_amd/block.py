@@ -35,6 +35,7 @@ import torch.nn as nn
 
 from . import _native as nat
 from .kernels.quaternion_norm import QuaternionLayerNorm
+from .kernels import ssm_fused as _sf
 from .kernels.ssm_fused import ssm_forward_front_dl, ssm_forward_fused_dl, ssm_front
 from .layers.causal_conv1d import CausalConv1d, causal_conv1d_silu
 from .layers.quaternion_linear import quaternion_to_real_projection, real_to_quaternion_projection
@@ -145,13 +146,129 @@ def bc_slice_width(batch: int, seq_len: int, d_inner: int, d_state: int, elsize:
     return max(1, min(d_inner, budget // max(per_d, 1)))
 
 
+class _SlicedBCTrain(torch.autograd.Function):
+    """The front and the SSM of the block with the B and C projections computed
+    d-slice by d-slice, differentiable, without B, C, dB or dC ever whole.
+
+    Forward: delta, s from the front (HIP); per slice, the two projection GEMMs
+    into reused buffers and the SSM's inference walk over that slice. Only the
+    inputs are saved. Backward, per slice: the two GEMMs again, the SSM's
+    training walk (its fp32 checkpoints, slice-sized), the SSM backward, then
+    the slice's weight gradients (dB_s^T x, written in place) and its share of
+    dx (dB_s W_s, accumulated in fp32); finally the front's backward. Against
+    whole projections this costs two GEMMs and one SSM walk more per step and
+    holds O(slice) memory for everything of size batch x seq_len x d_inner x
+    d_state.
+    """
+
+    @staticmethod
+    def forward(ctx, x_act, dt_raw, g_raw, wb, wc, lam_a, lam_i, dskip, h0, width, d_state,
+                eps, dtype):
+        b, t, D = x_act.shape
+        S = d_state
+        dt, g, xv = _sf._front_operands(dt_raw, g_raw, x_act)
+        delta, s = _sf._front_forward(dt, g, xv)
+        x2 = x_act.detach().reshape(b * t, D).to(dtype)
+        la, li, dv = (nat.param_f32(p) for p in (lam_a, lam_i, dskip))
+        buf = torch.empty(2, b * t * width * S * 4, device=x_act.device, dtype=dtype)
+        y = torch.empty(b, t, D, 4, device=x_act.device, dtype=dtype)
+        h_last = torch.empty(b, D, S, 4, device=x_act.device, dtype=torch.float32)
+        with torch.autocast(x_act.device.type, enabled=False):
+            _SlicedBCTrain._walks(x2, wb, wc, buf, delta, s, la, li, dv, h0, y, h_last, width,
+                                  S, eps, dtype)
+        ctx.save_for_backward(x_act, dt_raw, g_raw, wb, wc, lam_a, lam_i, dskip, h0)
+        ctx.meta = (width, S, eps, dtype)
+        return y, h_last
+
+    @staticmethod
+    def _walks(x2, wb, wc, buf, delta, s, la, li, dv, h0, y, h_last, width, S, eps, dtype):
+        b, t, D = delta.shape
+        for d0 in range(0, D, width):
+            n = min(width, D - d0)
+            bs, cs = _SlicedBCTrain._bc(x2, wb, wc, buf, d0, n, S, dtype)
+            ys, hs = ssm_forward_fused_dl(
+                delta[:, :, d0:d0 + n], s[:, :, d0:d0 + n], bs.view(b, t, n, S, 4),
+                cs.view(b, t, n, S, 4), la[d0:d0 + n], li[d0:d0 + n], dv[d0:d0 + n], eps=eps,
+                h0=None if h0 is None else h0[:, d0:d0 + n].detach(), return_state=True)
+            y[:, :, d0:d0 + n] = ys
+            h_last[:, d0:d0 + n] = hs
+
+    @staticmethod
+    def _bc(x2, wb, wc, buf, d0, n, S, dtype):
+        r0, r1 = d0 * S * 4, (d0 + n) * S * 4
+        m = x2.shape[0]
+        bs = buf[0, : m * n * S * 4].view(m, n * S * 4)
+        cs = buf[1, : m * n * S * 4].view(m, n * S * 4)
+        torch.mm(x2, wb.detach()[r0:r1].to(dtype).t(), out=bs)
+        torch.mm(x2, wc.detach()[r0:r1].to(dtype).t(), out=cs)
+        return bs, cs
+
+    @staticmethod
+    def backward(ctx, gy, gh_last):
+        x_act, dt_raw, g_raw, wb, wc, lam_a, lam_i, dskip, h0 = ctx.saved_tensors
+        width, S, eps, dtype = ctx.meta
+        b, t, D = x_act.shape
+        m = b * t
+        dev = x_act.device
+        dt, g, xv = _sf._front_operands(dt_raw, g_raw, x_act)
+        delta, s = _sf._front_forward(dt, g, xv)
+        x2 = x_act.detach().reshape(m, D).to(dtype)
+        la, li, dv = (nat.param_f32(p) for p in (lam_a, lam_i, dskip))
+        f32 = torch.float32
+        wide = {} if dtype == f32 else {"out_dtype": f32}
+        d_delta = torch.empty(b, t, D, device=dev, dtype=f32)
+        d_s = torch.empty(b, t, D, device=dev, dtype=f32)
+        dla = torch.empty(D, S, device=dev, dtype=f32)
+        dli = torch.empty(D, S, 3, device=dev, dtype=f32)
+        dD = torch.empty(D, device=dev, dtype=f32)
+        dh0 = None if h0 is None else torch.empty(b, D, S, 4, device=dev, dtype=f32)
+        dwb = torch.empty(wb.shape, device=dev, dtype=f32)
+        dwc = torch.empty(wc.shape, device=dev, dtype=f32)
+        dx2 = torch.zeros(m, D, device=dev, dtype=f32)
+        buf = torch.empty(2, m * width * S * 4, device=dev, dtype=dtype)
+        gy = gy if gy is not None else torch.zeros(b, t, D, 4, device=dev, dtype=dtype)
+        for d0 in range(0, D, width):
+            n = min(width, D - d0)
+            r0, r1 = d0 * S * 4, (d0 + n) * S * 4
+            bs, cs = _SlicedBCTrain._bc(x2, wb, wc, buf, d0, n, S, dtype)
+            _, _, saved = _sf.ssm_fused_dl_train_forward(
+                delta[:, :, d0:d0 + n], s[:, :, d0:d0 + n], bs.view(b, t, n, S, 4),
+                cs.view(b, t, n, S, 4), la[d0:d0 + n], li[d0:d0 + n], dv[d0:d0 + n],
+                None if h0 is None else h0[:, d0:d0 + n].detach(), eps)
+            dd, dss, dB, dC, dla_s, dli_s, dD_s, dh0_s = _sf.ssm_fused_dl_backward(
+                saved, gy[:, :, d0:d0 + n],
+                None if gh_last is None else gh_last[:, d0:d0 + n], eps)
+            del saved
+            d_delta[:, :, d0:d0 + n] = dd
+            d_s[:, :, d0:d0 + n] = dss
+            dla[d0:d0 + n] = dla_s
+            dli[d0:d0 + n] = dli_s
+            dD[d0:d0 + n] = dD_s
+            if dh0 is not None:
+                dh0[:, d0:d0 + n] = dh0_s
+            dB2 = dB.view(m, n * S * 4)
+            dC2 = dC.view(m, n * S * 4)
+            torch.mm(dB2.t(), x2, **wide, out=dwb[r0:r1])
+            torch.mm(dC2.t(), x2, **wide, out=dwc[r0:r1])
+            dx2.add_(torch.mm(dB2, wb.detach()[r0:r1].to(dtype), **wide))
+            dx2.add_(torch.mm(dC2, wc.detach()[r0:r1].to(dtype), **wide))
+            del dB, dC, dB2, dC2
+        d_dt, d_g, d_x = _sf._front_backward(dt, g, xv, d_delta, d_s)
+        dx = d_x.float().add_(dx2.view(b, t, D))
+        return (dx.to(x_act.dtype), d_dt.to(dt_raw.dtype), d_g.to(g_raw.dtype),
+                dwb.to(wb.dtype), dwc.to(wc.dtype), dla.to(lam_a.dtype), dli.to(lam_i.dtype),
+                dD.to(dskip.dtype), None if dh0 is None else dh0.to(h0.dtype),
+                None, None, None, None)
+
+
 class QuaternionMamba2Block(nn.Module):
     """One Quaternion Mamba-2 block. Input and output: [batch, seq_len, d_model].
 
-    bc_slice_d (attribute, not a parameter): None lets the inference forward
-    slice the B/C projections only when whole ones would exceed
-    BC_WHOLE_MAX_BYTES; an int forces slices of that many d's (inference only);
-    0 never slices.
+    bc_slice_d (attribute, not a parameter): None lets the forward slice the
+    B/C projections only when whole ones would exceed BC_WHOLE_MAX_BYTES; an
+    int forces slices of that many d's; 0 never slices. Inference slices run
+    the SSM per slice; training slices (_SlicedBCTrain) also recompute each
+    slice's projections in the backward.
     """
 
     def __init__(self, d_model: int, d_state: int = 64, d_conv: int = 4,
@@ -223,6 +340,15 @@ class QuaternionMamba2Block(nn.Module):
         dt_raw = self.dt_proj(x)
         g_raw = self.gate_proj(x)
         if width:
+            if torch.is_grad_enabled() and (x.requires_grad or any(
+                    p.requires_grad for p in self.parameters())):
+                if self.B_proj.bias is not None or self.C_proj.bias is not None:
+                    raise ValueError("sliced B/C projections take bias-free B_proj and C_proj")
+                nat.require_device("QuaternionMamba2Block", x, dt_raw, g_raw)
+                y, h = _SlicedBCTrain.apply(
+                    x, dt_raw, g_raw, self.B_proj.weight, self.C_proj.weight, self.Lambda_alpha,
+                    self.Lambda_imag, self.D, h0, width, self.d_state, 1e-6, self._gemm_dtype(x))
+                return (y, h) if return_state else y
             return self._ssm_forward_sliced(x, dt_raw, g_raw, width, h0, return_state)
         Bq = self.B_proj(x).view(b, t, D, self.d_state, 4)
         Cq = self.C_proj(x).view(b, t, D, self.d_state, 4)
@@ -246,10 +372,11 @@ class QuaternionMamba2Block(nn.Module):
             if forced < 0:
                 raise ValueError(f"bc_slice_d must be >= 0 or None, got {forced}")
             if recording:
-                raise ValueError("bc_slice_d: sliced B/C projections are inference-only "
-                                 "(the backward needs B and C whole)")
+                _sf._require_trainable_state(torch.empty(0, self.d_state, 4))
             return min(int(forced), self.d_inner)
-        if recording or self.B_proj.bias is not None or self.C_proj.bias is not None:
+        if self.B_proj.bias is not None or self.C_proj.bias is not None:
+            return 0
+        if recording and self.d_state > _sf.SSM_BWD_MAX_STATE:
             return 0
         b, t, D = x.shape
         el = 4 if self._gemm_dtype(x) == torch.float32 else 2

@@ -81,7 +81,7 @@ def test_sliced_state_pieces(dtype, rtol):
 
 def test_sliced_auto_rule(monkeypatch):
     """With the whole-projection bound lowered below this input's B and C, the
-    inference forward slices by itself, with the width bc_slice_width gives."""
+    forward slices by itself, with the width bc_slice_width gives."""
     blk = _block(64, 16, torch.float32, seed=3)
     x = torch.randn(2, 128, 64, device=DEV)
     with torch.no_grad():
@@ -97,6 +97,85 @@ def test_sliced_auto_rule(monkeypatch):
         forced = blk(x)
     assert torch.equal(got, forced)
     assert_close(got, whole, 1e-5, "auto-sliced vs whole")
-    # Training never slices on its own.
+    # Training slices by the same rule (through _SlicedBCTrain).
     blk.bc_slice_d = None
-    assert blk._bc_slice_width(x_act.clone().requires_grad_()) == 0
+    assert blk._bc_slice_width(x_act.clone().requires_grad_()) == 12
+
+
+def _train_grads(blk, x, gy, state=None):
+    params = [p for p in blk.parameters()]
+    if state is None:
+        y = blk(x)
+        outs, grads_of = (y,), (gy,)
+        ins = [x] + params
+    else:
+        y, (_, h) = blk.forward_with_state(x, state)
+        outs, grads_of = (y, h), (gy, torch.ones_like(h))
+        ins = [x, state[1]] + params
+    return outs, torch.autograd.grad(outs, ins, grads_of)
+
+
+@pytest.mark.parametrize("dtype,rtol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("width", [7, 128])
+def test_sliced_training_equals_whole(dtype, rtol, width):
+    """Training through _SlicedBCTrain (B/C per slice, recomputed in the
+    backward) against whole projections: output and every gradient."""
+    blk = _block(64, 16, dtype, seed=6)
+    x = torch.randn(2, 70, 64, generator=torch.Generator(device=DEV).manual_seed(7),
+                    device=DEV).to(dtype)
+    gy = torch.randn(2, 70, 64, generator=torch.Generator(device=DEV).manual_seed(8),
+                     device=DEV).to(dtype)
+    blk.bc_slice_d = 0
+    (yw,), gw = _train_grads(blk, x.clone().requires_grad_(), gy)
+    blk.bc_slice_d = width
+    (ys,), gs = _train_grads(blk, x.clone().requires_grad_(), gy)
+    assert_close(ys, yw, rtol, f"sliced training forward w{width}")
+    names = ["x"] + [n for n, _ in blk.named_parameters()]
+    for n, a, b in zip(names, gs, gw):
+        assert_close(a, b, max(rtol, 1e-4), f"sliced training grad {n} w{width}")
+
+
+def test_sliced_training_autocast_and_state():
+    """fp32 parameters under fp16 autocast (the config-4 setting) and a
+    recurrent state with gradients (h0 and h_last), sliced against whole."""
+    blk = _block(64, 16, torch.float32, seed=9)
+    g = torch.Generator(device=DEV).manual_seed(10)
+    x = torch.randn(2, 50, 64, generator=g, device=DEV)
+    gy = torch.randn(2, 50, 64, generator=g, device=DEV)
+    tail = torch.randn(2, 3, 128, generator=g, device=DEV)
+    h0 = torch.randn(2, 128, 16, 4, generator=g, device=DEV) * 0.1
+    res = {}
+    for width in (0, 9):
+        blk.bc_slice_d = width
+        with torch.autocast("cuda", dtype=torch.float16):
+            res[width] = _train_grads(blk, x.clone().requires_grad_(), gy.half(),
+                                      (tail, h0.clone().requires_grad_()))
+    (yw, hw), gw = res[0]
+    (ys, hs), gs = res[9]
+    assert_close(ys, yw, 2e-2, "autocast sliced forward")
+    assert_close(hs, hw, 1e-3, "autocast sliced h_last")
+    names = ["x", "h0"] + [n for n, _ in blk.named_parameters()]
+    for n, a, b in zip(names, gs, gw):
+        assert_close(a, b, 2e-2, f"autocast sliced grad {n}")
+
+
+def test_sliced_training_memory_bound():
+    """Peak memory of a training step with 32-d slices stays well under the
+    whole-projection step's (B, C, dB, dC at B1 T4096 d_inner 512 S64 bf16:
+    2.1 GB each pair)."""
+    blk = _block(256, 64, torch.bfloat16, seed=11)
+    x = torch.randn(1, 4096, 256, device=DEV).to(torch.bfloat16)
+    peaks = {}
+    for width in (0, 32):
+        blk.bc_slice_d = width
+        blk.zero_grad(set_to_none=True)
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        y = blk(x.clone().requires_grad_())
+        y.float().pow(2).mean().backward()
+        torch.cuda.synchronize()
+        peaks[width] = torch.cuda.max_memory_allocated() - base
+        del y
+    assert peaks[32] < peaks[0] / 2, peaks

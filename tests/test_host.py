@@ -348,8 +348,8 @@ def test_build_rejects_kernels_that_spill():
 
 def test_bc_slice_rule():
     """The sliced B/C rule without a GPU: widths from the byte budget, whole
-    projections below the bound, and forced slicing refused when autograd
-    records (the backward needs B and C whole)."""
+    projections below the bound, forced widths, and training slices refused
+    beyond the backward's d_state limit."""
     import mambaqc_amd
     from mambaqc_amd import block as bm
     assert bm.bc_slice_width(1, 262144, 1536, 64, 2) == 8
@@ -366,11 +366,18 @@ def test_bc_slice_rule():
         blk.bc_slice_d = -1
         with pytest.raises(ValueError):
             blk._bc_slice_width(x)
+    # Training slices too (the backward recomputes each slice's projections),
+    # while d_state is within the backward's limit.
     blk.bc_slice_d = 5
-    with pytest.raises(ValueError, match="inference-only"):
-        blk._bc_slice_width(x)
+    assert blk._bc_slice_width(x) == 5
     blk.bc_slice_d = None
     assert blk._bc_slice_width(x) == 0
+    big = mambaqc_amd.QuaternionMamba2Block(16, d_state=128)
+    big.bc_slice_d = 4
+    with pytest.raises(ValueError, match="d_state <= 64"):
+        big._bc_slice_width(torch.zeros(1, 4, 32))
+    with torch.no_grad():
+        assert big._bc_slice_width(torch.zeros(1, 4, 32)) == 4
 
 
 def test_torch_ops_registered_with_fake_kernels():
