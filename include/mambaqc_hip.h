@@ -269,6 +269,40 @@ int mqc_ssm_fused_bwd(const void* delta, const void* s, const void* B, const voi
                       void* dh0, int64_t batch, int64_t seq_len, int64_t d_inner,
                       int64_t d_state, float eps, int dtype, void* stream);
 
+/* mqc_ssm_fused_fwd_train with the seq axis cut into chunks of chunk_len steps
+ * walked side by side (for batch x d_inner x d_state too small to fill the GPU,
+ * as in mqc_ssm_fused_fwd_chunked). chunk_len must be a multiple of ckpt_every
+ * (the checkpoints are the whole walk's, at the same steps); workspace holds
+ * mqc_ssm_chunked_workspace_bytes(batch, seq_len, d_inner, d_state, chunk_len)
+ * bytes (16-byte aligned; MQC_E_SPACE if smaller); d_state <= 64. chunk_len >=
+ * seq_len is the whole walk (no workspace used). No counterpart in the
+ * reference (its GPU path has no training forward). */
+int mqc_ssm_fused_fwd_train_chunked(const void* delta, const void* s, const void* B,
+                                    const void* C, const float* lambda_alpha,
+                                    const float* lambda_imag, const float* D, const void* h0,
+                                    void* y, void* h_last, float* h_ckpt, int64_t ckpt_every,
+                                    int64_t batch, int64_t seq_len, int64_t d_inner,
+                                    int64_t d_state, int64_t chunk_len, float eps, int dtype,
+                                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* mqc_ssm_fused_bwd with the seq axis cut into chunks of chunk_len steps run
+ * side by side: the adjoint entering each chunk comes from a reverse carry
+ * pass over the chunks after it (same workspace size and chunk_len rule as
+ * mqc_ssm_fused_fwd_train_chunked). With n_chunks = ceil(seq_len / chunk_len)
+ * > 1 the parameter partials have n_chunks * batch rows
+ * (dlambda_alpha_part fp32 [n_chunks * batch, d_inner, d_state], and so on; the
+ * caller sums the first axis); chunk_len >= seq_len is mqc_ssm_fused_bwd. No
+ * counterpart in the reference. */
+int mqc_ssm_fused_bwd_chunked(const void* delta, const void* s, const void* B, const void* C,
+                              const float* lambda_alpha, const float* lambda_imag, const float* D,
+                              const void* h0, const float* h_ckpt, int64_t ckpt_every,
+                              const void* gy, const void* dh_last, float* d_delta, float* d_s,
+                              void* dB, void* dC, float* dlambda_alpha_part,
+                              float* dlambda_imag_part, float* dD_part, void* dh0, int64_t batch,
+                              int64_t seq_len, int64_t d_inner, int64_t d_state,
+                              int64_t chunk_len, float eps, int dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
 /* Backward of mqc_qln_fwd given dout (dtype [rows, d, 4]) and the forward's
  * saved mean and rstd: writes dq (dtype [rows, d, 4]) and
  * ne = n-hat * <dout, q / (n + eps)> (fp32 [rows, d]); dgamma = sum over rows

@@ -58,6 +58,12 @@ SIGNATURES = {
     "mqc_ssm_fused_fwd_chunked": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp, _i64, _vp],
     "mqc_gemm_nt": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
+    "mqc_ssm_fused_fwd_train_chunked": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                        _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp,
+                                        _i64, _vp],
+    "mqc_ssm_fused_bwd_chunked": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp,
+                                  _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                                  _i64, _i64, _f32, _int, _vp, _i64, _vp],
     "mqc_ssm_fused_fwd_chunked_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                           _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp],
 }

@@ -67,6 +67,16 @@ struct SsmBwdArgs {
   float* dh0;              // [B,D,S,4] fp32 or null
   int64_t batch, T, Dm, S;
   float eps;
+  // Time-chunked backward (ssm_bwd_chunked_launch): the T axis in n_chunks
+  // chunks of chunk_len steps (a multiple of the checkpoint interval; the last
+  // may be shorter), one row of blocks per (chunk, batch). The last chunk starts
+  // from dh_last, chunk c < n_chunks - 1 from e_chunk[b, n_chunks - 2 - c]
+  // (fp32 [B, n_chunks - 1, D, S, 4]: the adjoint flowing into its last step
+  // from the chunks after it). The parameter partials then have
+  // n_chunks * batch rows (row chunk * batch + b) and only chunk 0 writes dh0.
+  int64_t chunk_len = 0;
+  int64_t n_chunks = 1;
+  const float* e_chunk = nullptr;
 };
 
 // Pull dq back through q = Cayley(dl * Lambda) (closed form, see ssm_scan.hpp):
@@ -170,7 +180,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
   // The write excess (1.024x) is the fp32 d_delta / d_s rows: a block holds 4
   // d's, 16 bytes of each row, which leave the L2 as 12.6 M masked 32-byte
   // writes (TCC_EA0_WRREQ minus TCC_EA0_WRREQ_64B), 0.44 GB for 0.1 GB of data.
-  const int64_t b = blockIdx.y;
+  const int64_t by = blockIdx.y;
+  const int chunk = a.n_chunks > 1 ? (int)(by / a.batch) : 0;
+  const int64_t b = a.n_chunks > 1 ? by - (int64_t)chunk * a.batch : by;
   const int64_t d_raw = (int64_t)blockIdx.x * GPB + tid / G;
   const bool gvalid = d_raw < a.Dm;
   const int64_t d = gvalid ? d_raw : a.Dm - 1;
@@ -197,7 +209,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
   PullAcc pacc;
   float dD = 0.f;
   quat carry{0.f, 0.f, 0.f, 0.f};
-  if (a.dh_last) {
+  if (chunk < a.n_chunks - 1) {
+    const int64_t ci = ((b * (a.n_chunks - 1) + (a.n_chunks - 2 - chunk)) * a.Dm + d) * a.S + k;
+    float e[4];
+    load_vec<float, 4>(a.e_chunk + ci * 4, e);
+    carry = quat_from(e);
+  } else if (a.dh_last) {
     float e[4];
     load_vec<float, 4>(a.dh_last + sidx, e);
     carry = quat_from(e);
@@ -336,23 +353,28 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
     if constexpr (SYNC) __syncthreads();
   };
 
+  // This block's checkpoint chunks: [c_lo, c_end) (all of them unchunked).
+  const int Lc = a.n_chunks > 1 ? (int)a.chunk_len : Tn;
+  const int c_lo = a.n_chunks > 1 ? chunk * (Lc / K) : 0;
+  const int c_end = chunk == a.n_chunks - 1 ? nC : (chunk + 1) * (Lc / K);
   Ops buf;
-  if (nC > 0) {
-    const int c = nC - 1;
-    const int len = (int)(Tn - c * K);
+  if (c_end > c_lo) {
+    const int c = c_end - 1;
+    const int len = (int)(Tn - c * K) < K ? (int)(Tn - c * K) : K;
     load_chunk(buf, c, len);
     if (len == K)
       process_chunk(std::integral_constant<bool, true>{}, buf, c, len);
     else
       process_chunk(std::integral_constant<bool, false>{}, buf, c, len);
   }
-  for (int c = nC - 2; c >= 0; --c) {
+  for (int c = c_end - 2; c >= c_lo; --c) {
     load_chunk(buf, c, K);
     process_chunk(std::integral_constant<bool, true>{}, buf, c, K);
   }
 
+  const int64_t prow = (int64_t)chunk * a.batch + b;  // partials row
   if (own) {
-    if (a.dh0) {
+    if (a.dh0 && chunk == 0) {
       const float e[4] = {carry.w, carry.x, carry.y, carry.z};
       store_vec<float, 4>(a.dh0 + sidx, e);
     }
@@ -361,13 +383,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
     // Chain to the raw parameters: a = -softplus(alpha), v = tanh(imag).
     const float alpha = a.lam_alpha[dk];
     const float sig = alpha > 20.f ? 1.f : 1.f / (1.f + expf(-alpha));
-    a.dalpha_part[b * a.Dm * a.S + dk] = -da * sig;
-    float* di = a.dimag_part + (b * a.Dm * a.S + dk) * 3;
+    a.dalpha_part[prow * a.Dm * a.S + dk] = -da * sig;
+    float* di = a.dimag_part + (prow * a.Dm * a.S + dk) * 3;
     di[0] = dv[0] * (1.f - L.v0 * L.v0);
     di[1] = dv[1] * (1.f - L.v1 * L.v1);
     di[2] = dv[2] * (1.f - L.v2 * L.v2);
   }
-  if (gvalid && j == 0) a.dD_part[b * a.Dm + d] = dD;
+  if (gvalid && j == 0) a.dD_part[prow * a.Dm + d] = dD;
 }
 
 // Checkpoint interval the backward needs: the chunk's operands and states live
@@ -381,8 +403,9 @@ int launch_ssm_bwd_g(const SsmBwdArgs& a, hipStream_t s) {
   constexpr int NT = 256;
   constexpr int GPB = NT / G;
   const int64_t gx = (a.Dm + GPB - 1) / GPB;
-  if (gx > 0x7fffffffLL || a.batch > 65535) return MQC_E_LIMIT;
-  const dim3 grid((unsigned)gx, (unsigned)a.batch);
+  const int64_t gy = a.batch * a.n_chunks;  // (chunk, batch) rows
+  if (gx > 0x7fffffffLL || gy > 65535) return MQC_E_LIMIT;
+  const dim3 grid((unsigned)gx, (unsigned)gy);
   if (a.S == G)
     ssm_bwd_kernel<T, G, K, NT, true, false><<<grid, dim3(NT), 0, s>>>(a);
   else

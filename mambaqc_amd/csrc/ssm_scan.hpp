@@ -381,11 +381,14 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   const bool writer = gvalid && (G < 4 || j < 4);
   const int64_t rowY = a.Dm * 4;
   const uint32_t offY = (uint32_t)(d * 4 * (int64_t)sizeof(T));
-  // Checkpoint schedule (scalar): the next step whose state is saved.
+  // Checkpoint schedule (scalar): the next step whose state is saved. A chunk
+  // of the time-chunked walk starts on a checkpoint boundary (the host keeps
+  // chunk_len a multiple of ckpt_every), so its first checkpoint is the one
+  // that ends tb + ckpt_every - 1.
   const int ckpt_every = (int)a.ckpt_every;
   const int64_t n_ckpt = a.h_ckpt ? (Tn + ckpt_every - 1) / ckpt_every : 0;
-  int next_ckpt = a.h_ckpt ? (ckpt_every < Tn ? ckpt_every - 1 : Tn - 1) : -1;
-  int64_t ckpt_idx = 0;
+  int next_ckpt = a.h_ckpt ? (tb + ckpt_every - 1 < Tn ? tb + ckpt_every - 1 : Tn - 1) : -1;
+  int64_t ckpt_idx = a.h_ckpt ? tb / ckpt_every : 0;
 
   // One step t from ring slot cur.
   auto walk_step = [&](auto refill, Step<T, MODE, KPL>& cur, int t) {

@@ -135,13 +135,35 @@ def _require_trainable_state(B: torch.Tensor) -> None:
             f"(got {d_state}); run without autograd (torch.no_grad) for inference")
 
 
+def train_chunk_len(batch: int, seq_len: int, d_inner: int, d_state: int,
+                    dtype: torch.dtype, chunk_len: int | None = None) -> int:
+    """Chunk length of the training walk and the backward: the inference
+    walk's choice (chunk_len_for) or `chunk_len`, rounded up to a multiple of
+    the checkpoint interval (seq_len or more: the whole walk)."""
+    code = nat.dtype_code(torch.empty(0, dtype=dtype))
+    K = int(nat.load().mqc_ssm_bwd_ckpt_every(code))
+    if chunk_len is not None and int(chunk_len) < 1:
+        raise ValueError(f"chunk_len must be >= 1, got {chunk_len}")
+    L = chunk_len_for(batch, seq_len, d_inner, d_state, dtype) if chunk_len is None \
+        else int(chunk_len)
+    return -(-L // K) * K
+
+
+def _chunk_workspace(batch, T, d_inner, d_state, L, device):
+    nbytes = int(nat.load().mqc_ssm_chunked_workspace_bytes(batch, T, d_inner, d_state, L))
+    if nbytes < 0:
+        nat.check(nbytes, "mqc_ssm_chunked_workspace_bytes")
+    return torch.empty(max(nbytes, 16), device=device, dtype=torch.uint8), nbytes
+
+
 def ssm_fused_dl_train_forward(delta, s, B, C, lambda_alpha, lambda_imag, D, h0=None,
-                               eps: float = 1e-6):
+                               eps: float = 1e-6, chunk_len: int | None = None):
     """Training forward of the block's SSM: y, the final state, and what the
     backward needs (the kernel operands and the fp32 state checkpoints).
 
     Returns (y, h_last, saved) with saved = (delta, s, B, C, lambda_alpha,
-    lambda_imag, D, h0, checkpoints) in the kernel's types.
+    lambda_imag, D, h0, checkpoints) in the kernel's types. Small batches walk
+    in time chunks (train_chunk_len; chunk_len forces a length).
     """
     _require_trainable_state(B)
     batch, T, d_inner, d_state = _dl_check(delta, s, B, C, lambda_alpha, lambda_imag, D, h0)
@@ -154,14 +176,24 @@ def ssm_fused_dl_train_forward(delta, s, B, C, lambda_alpha, lambda_imag, D, h0=
     h_last = torch.empty(batch, d_inner, d_state, 4, device=Bc.device, dtype=torch.float32)
     ckpt = torch.empty(batch, max(n_ckpt, 1), d_inner, d_state, 4, device=Bc.device,
                        dtype=torch.float32)
-    nat.call("mqc_ssm_fused_fwd_train", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
-             Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
-             y.data_ptr(), h_last.data_ptr(), ckpt.data_ptr(), K, batch, T, d_inner, d_state,
-             float(eps), code, nat.stream_of(Bc))
+    L = train_chunk_len(batch, T, d_inner, d_state, Bc.dtype, chunk_len)
+    if 0 < L < T:
+        ws, nbytes = _chunk_workspace(batch, T, d_inner, d_state, L, Bc.device)
+        nat.call("mqc_ssm_fused_fwd_train_chunked", Bc, dl.data_ptr(), sv.data_ptr(),
+                 Bc.data_ptr(), Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(),
+                 nat.ptr(h0c), y.data_ptr(), h_last.data_ptr(), ckpt.data_ptr(), K, batch, T,
+                 d_inner, d_state, L, float(eps), code, ws.data_ptr(), nbytes,
+                 nat.stream_of(Bc))
+    else:
+        nat.call("mqc_ssm_fused_fwd_train", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
+                 Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
+                 y.data_ptr(), h_last.data_ptr(), ckpt.data_ptr(), K, batch, T, d_inner,
+                 d_state, float(eps), code, nat.stream_of(Bc))
     return y, h_last, (dl, sv, Bc, Cc, la, li, Dv, h0c, ckpt)
 
 
-def ssm_fused_dl_backward(saved, gy, gh_last=None, eps: float = 1e-6):
+def ssm_fused_dl_backward(saved, gy, gh_last=None, eps: float = 1e-6,
+                          chunk_len: int | None = None):
     """Backward of ssm_fused_dl_train_forward given dL/dy (and dL/dh_last).
 
     Returns (d_delta, d_s fp32 [batch, T, d_inner], dB, dC in B's dtype,
@@ -181,16 +213,27 @@ def ssm_fused_dl_backward(saved, gy, gh_last=None, eps: float = 1e-6):
     d_s = torch.empty(sv.shape, device=dev, dtype=torch.float32)
     dB = torch.empty_like(Bc)
     dC = torch.empty_like(Cc)
-    dla = torch.empty(batch, d_inner, d_state, device=dev, dtype=torch.float32)
-    dli = torch.empty(batch, d_inner, d_state, 3, device=dev, dtype=torch.float32)
-    dD = torch.empty(batch, d_inner, device=dev, dtype=torch.float32)
+    L = train_chunk_len(batch, T, d_inner, d_state, dtype, chunk_len)
+    rows = batch * (-(-T // L)) if 0 < L < T else batch  # partials: (chunk, batch) rows
+    dla = torch.empty(rows, d_inner, d_state, device=dev, dtype=torch.float32)
+    dli = torch.empty(rows, d_inner, d_state, 3, device=dev, dtype=torch.float32)
+    dD = torch.empty(rows, d_inner, device=dev, dtype=torch.float32)
     dh0 = torch.empty_like(h0c) if h0c is not None else None
-    nat.call("mqc_ssm_fused_bwd", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
-             Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
-             ckpt.data_ptr(), K, gy.data_ptr(), nat.ptr(gh_last), d_delta.data_ptr(),
-             d_s.data_ptr(), dB.data_ptr(), dC.data_ptr(), dla.data_ptr(), dli.data_ptr(),
-             dD.data_ptr(), nat.ptr(dh0), batch, T, d_inner, d_state, float(eps), code,
-             nat.stream_of(Bc))
+    if 0 < L < T:
+        ws, nbytes = _chunk_workspace(batch, T, d_inner, d_state, L, dev)
+        nat.call("mqc_ssm_fused_bwd_chunked", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
+                 Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
+                 ckpt.data_ptr(), K, gy.data_ptr(), nat.ptr(gh_last), d_delta.data_ptr(),
+                 d_s.data_ptr(), dB.data_ptr(), dC.data_ptr(), dla.data_ptr(), dli.data_ptr(),
+                 dD.data_ptr(), nat.ptr(dh0), batch, T, d_inner, d_state, L, float(eps), code,
+                 ws.data_ptr(), nbytes, nat.stream_of(Bc))
+    else:
+        nat.call("mqc_ssm_fused_bwd", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(),
+                 Cc.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(), nat.ptr(h0c),
+                 ckpt.data_ptr(), K, gy.data_ptr(), nat.ptr(gh_last), d_delta.data_ptr(),
+                 d_s.data_ptr(), dB.data_ptr(), dC.data_ptr(), dla.data_ptr(), dli.data_ptr(),
+                 dD.data_ptr(), nat.ptr(dh0), batch, T, d_inner, d_state, float(eps), code,
+                 nat.stream_of(Bc))
     return d_delta, d_s, dB, dC, dla.sum(0), dli.sum(0), dD.sum(0), dh0
 
 

@@ -29,7 +29,7 @@ def declared_symbols():
 
 def test_header_declares_the_api():
     names = declared_symbols()
-    assert len(names) == 28, names
+    assert len(names) == 30, names
     assert set(nat.SIGNATURES) | set(nat.SIGNATURES_I64) <= set(names)
 
 
@@ -421,3 +421,30 @@ def test_torch_ops_registered_with_fake_kernels():
     assert sh(mm.out_gate(m(2, 5, 8), m(2, 5, 16, dt=bf), m(2, 5, 8, dt=bf))) == [((2, 5, 8), torch.float32)]
     with pytest.raises(RuntimeError):
         mm.quaternion_multiply(torch.zeros(2, 4), torch.zeros(2, 4))
+
+
+def test_chunked_training_validation_without_gpu():
+    """The chunked training entry points refuse, before any HIP call, a chunk
+    length that is not a multiple of the checkpoint interval, a short
+    workspace and d_state above 64; the Python rule rounds chunk lengths up to
+    that interval."""
+    from mambaqc_amd.kernels.ssm_fused import train_chunk_len
+    lib = nat.load()
+    bf = 1
+    K = lib.mqc_ssm_bwd_ckpt_every(bf)
+    assert K == 8
+    P = [FAKE] * 11
+    # (…, ckpt_every, batch, seq_len, d_inner, d_state, chunk_len, eps, dtype, ws, ws_bytes, stream)
+    assert lib.mqc_ssm_fused_fwd_train_chunked(*P, K, 1, 100, 4, 8, 12, 1e-6, bf, FAKE, 1 << 20, None) == -2
+    assert lib.mqc_ssm_fused_fwd_train_chunked(*P, K, 1, 100, 4, 8, 0, 1e-6, bf, FAKE, 1 << 20, None) == -2
+    assert lib.mqc_ssm_fused_fwd_train_chunked(*P, K, 1, 100, 4, 8, 16, 1e-6, bf, FAKE, 0, None) == -6
+    assert lib.mqc_ssm_fused_fwd_train_chunked(*P, K, 1, 100, 4, 128, 16, 1e-6, bf, FAKE, 1 << 30, None) == -5
+    Q = [FAKE] * 9
+    R = [FAKE] * 10
+    assert lib.mqc_ssm_fused_bwd_chunked(*Q, K, *R, 1, 100, 4, 8, 12, 1e-6, bf, FAKE, 1 << 20, None) == -2
+    assert lib.mqc_ssm_fused_bwd_chunked(*Q, K, *R, 1, 100, 4, 8, 16, 1e-6, bf, FAKE, 16, None) == -6
+    assert lib.mqc_ssm_fused_bwd_chunked(*Q, K, *R, 1, 100, 4, 8, 16, 1e-6, bf, None, 1 << 30, None) == -1
+    assert train_chunk_len(1, 2048, 1536, 64, torch.bfloat16) % 8 == 0
+    assert train_chunk_len(1, 2048, 1536, 64, torch.float32) % 4 == 0
+    assert train_chunk_len(1, 100, 4, 8, torch.bfloat16, chunk_len=13) == 16
+    assert train_chunk_len(4, 2048, 1536, 64, torch.bfloat16) >= 2048  # config 3: whole
