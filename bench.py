@@ -389,6 +389,7 @@ def run_full(args):
 
 
 LONG_T = 262144
+LONG_TRAIN_T = 65536
 
 
 def long_context_timing(blk):
@@ -418,11 +419,41 @@ def long_context_timing(blk):
         f"{width} d's per B/C slice, peak {peak / 2**30:.1f} GiB beyond the inputs")
     del x
     torch.cuda.empty_cache()
+    # Training at LONG_TRAIN_T tokens: slices recomputed in the backward, the
+    # SSM's training walk and backward in time chunks.
+    xt = torch.randn(1, LONG_TRAIN_T, DM, generator=g, device="cuda").to(torch.bfloat16)
+    wt = bm.bc_slice_width(1, LONG_TRAIN_T, DI, DS, 2)
+
+    def train_step():
+        blk.zero_grad(set_to_none=True)
+        blk(xt.clone().requires_grad_()).float().pow(2).mean().backward()
+
+    train_step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base_mem = torch.cuda.memory_allocated()
+    t0 = time.perf_counter()
+    for _ in range(2):
+        train_step()
+    torch.cuda.synchronize()
+    tms = (time.perf_counter() - t0) * 1e3 / 2
+    tpeak = torch.cuda.max_memory_allocated() - base_mem
+    blk.zero_grad(set_to_none=True)
+    log(f"long context training: B1 T{LONG_TRAIN_T} forward+backward {tms:.1f} ms "
+        f"({LONG_TRAIN_T / tms * 1e3:.0f} tokens/s), {wt} d's per slice, peak {tpeak / 2**30:.1f} GiB")
+    del xt
+    torch.cuda.empty_cache()
     return {"workload": f"QuaternionMamba2Block forward (config-3 width, bf16), batch 1, "
                         f"seq_len {LONG_T}, B/C projections in d-slices",
             "ms_per_step": round(ms, 2), "tokens_per_s": round(LONG_T / ms * 1e3, 1),
             "bc_slice_d": width, "whole_bc_bytes": 2 * LONG_T * DI * DS * 4 * 2,
-            "peak_alloc_GiB": round(peak / 2**30, 2)}
+            "peak_alloc_GiB": round(peak / 2**30, 2),
+            "train": {"workload": f"forward + backward, bf16, batch 1, seq_len {LONG_TRAIN_T}, "
+                                  f"B/C in d-slices recomputed in the backward, chunked SSM "
+                                  f"training walk and backward",
+                      "ms_per_step": round(tms, 2),
+                      "tokens_per_s": round(LONG_TRAIN_T / tms * 1e3, 1),
+                      "bc_slice_d": wt, "peak_alloc_GiB": round(tpeak / 2**30, 2)}}
 
 
 def train_timings(args):
