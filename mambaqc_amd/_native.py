@@ -182,11 +182,16 @@ def param_f32(t: torch.Tensor) -> torch.Tensor:
     model dtype). An fp32 tensor that already qualifies is used as is; other
     conversions are cached and redone when the tensor's data pointer, shape or
     version counter (bumped by every in-place update) changes. Inference
-    tensors have no version counter and are converted on every call."""
+    tensors, and any tensor while inference mode is on, are converted on every
+    call (the former have no version counter; a conversion made in inference
+    mode could not be saved for a later backward)."""
     if t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0:
         return t.detach()
-    if t.is_inference():
-        # No version counter to tell an in-place update: convert every time.
+    if t.is_inference() or torch.is_inference_mode_enabled():
+        # An inference tensor has no version counter to tell an in-place
+        # update; a conversion made in inference mode is an inference tensor,
+        # which autograd could not save if the cache handed it to a later
+        # training step. Both convert every time.
         return aligned16(t.detach().float())
     key = (t._version, t.data_ptr(), t.dtype, tuple(t.shape))
     hit = _F32_CACHE.get(id(t))

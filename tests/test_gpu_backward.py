@@ -330,3 +330,21 @@ def test_ssm_empty_sequence(dtype):
     assert torch.equal(got[7].grad.cpu(), gh)
     for t, name in zip(got[4:7], ["lambda_alpha", "lambda_imag", "D"]):
         assert t.grad is not None and (t.grad == 0).all(), name
+
+
+def test_training_after_inference_mode():
+    """A bf16 block run under torch.inference_mode, then trained: the library's
+    fp32 copies of its small parameters made in inference mode are not reused
+    by the training step (autograd could not save them)."""
+    torch.manual_seed(8)
+    blk = mambaqc_amd.QuaternionMamba2Block(32, d_state=8).to(DEV, torch.bfloat16)
+    x = torch.randn(2, 30, 32, device=DEV).to(torch.bfloat16)
+    with torch.inference_mode():
+        y0 = blk(x)
+    xr = x.clone().requires_grad_()
+    y = blk(xr)
+    y.float().pow(2).mean().backward()
+    # (the training walk and the inference walk sum over d_state in different orders)
+    assert_close(y, y0.clone(), 2e-2, "training forward after inference mode")
+    assert xr.grad is not None and torch.isfinite(xr.grad.float()).all()
+    assert all(p.grad is not None for p in blk.parameters())
