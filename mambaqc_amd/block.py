@@ -336,12 +336,14 @@ class QuaternionMamba2Block(nn.Module):
                      return_state: bool = False):
         """x: [batch, seq_len, d_inner] (real) -> y: [batch, seq_len, d_inner, 4]."""
         b, t, D = x.shape
-        width = self._bc_slice_width(x)
+        recording = torch.is_grad_enabled() and (
+            x.requires_grad or (h0 is not None and h0.requires_grad)
+            or any(p.requires_grad for p in self.parameters()))
+        width = self._bc_slice_width(x, recording)
         dt_raw = self.dt_proj(x)
         g_raw = self.gate_proj(x)
         if width:
-            if torch.is_grad_enabled() and (x.requires_grad or any(
-                    p.requires_grad for p in self.parameters())):
+            if recording:
                 if self.B_proj.bias is not None or self.C_proj.bias is not None:
                     raise ValueError("sliced B/C projections take bias-free B_proj and C_proj")
                 nat.require_device("QuaternionMamba2Block", x, dt_raw, g_raw)
@@ -361,13 +363,16 @@ class QuaternionMamba2Block(nn.Module):
             return torch.get_autocast_dtype(x.device.type)
         return x.dtype
 
-    def _bc_slice_width(self, x: torch.Tensor) -> int:
-        """d's per B/C slice for this input, 0 for whole projections."""
+    def _bc_slice_width(self, x: torch.Tensor, recording: bool | None = None) -> int:
+        """d's per B/C slice for this input, 0 for whole projections.
+        recording: whether autograd records this forward (None: judged from x
+        and the parameters)."""
         forced = self.bc_slice_d
         if forced == 0:
             return 0
-        recording = torch.is_grad_enabled() and (x.requires_grad or any(
-            p.requires_grad for p in self.parameters()))
+        if recording is None:
+            recording = torch.is_grad_enabled() and (x.requires_grad or any(
+                p.requires_grad for p in self.parameters()))
         if forced is not None:
             if forced < 0:
                 raise ValueError(f"bc_slice_d must be >= 0 or None, got {forced}")
