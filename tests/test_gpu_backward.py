@@ -248,6 +248,14 @@ def test_block_backward_ragged():
     _block_grads_vs_oracle(24, 5, 2, (2, 19, 24), seed=4)
 
 
+def test_block_backward_chunked_walks():
+    """Batch 1, 300 steps, 4 x 16 states: the SSM's training walk and backward
+    run in time chunks (train_chunk_len < seq_len), inside the block's autograd."""
+    from mambaqc_amd.kernels.ssm_fused import train_chunk_len
+    assert train_chunk_len(1, 300, 64, 16, torch.float32) < 300
+    _block_grads_vs_oracle(32, 16, 2, (1, 300, 32), seed=12)
+
+
 def test_block_forward_backward_config4_fp16_autocast():
     """Config 4 at full size: B4 T2048 d768 s64, fp16 autocast, forward +
     backward of the whole block, with loss scaling as torch's GradScaler does it
