@@ -413,11 +413,11 @@ int launch_ssm_bwd_g(const SsmBwdArgs& a, hipStream_t s) {
   return launch_status();
 }
 
+// What every launch of the backward needs of its arguments, checked on the
+// host before any kernel runs (the chunked backward calls it before its carry
+// launch).
 template <typename T>
-int launch_ssm_bwd(const SsmBwdArgs& a, hipStream_t s) {
-  // T == 0 still launches: the walk is empty, dh0 = dh_last and the parameter
-  // partials are zero.
-  if (a.batch == 0 || a.Dm == 0) return MQC_OK;
+int ssm_bwd_check(const SsmBwdArgs& a) {
   // K consecutive steps of one tensor must be addressable with 32-bit offsets.
   if (a.Dm * a.S * 4 * (int64_t)sizeof(T) * ssm_bwd_chunk<T>() >= ((int64_t)1 << 32))
     return MQC_E_LIMIT;
@@ -429,6 +429,16 @@ int launch_ssm_bwd(const SsmBwdArgs& a, hipStream_t s) {
       !aligned(a.delta, sizeof(T)) || !aligned(a.s, sizeof(T)) || !aligned(a.d_delta, 4) ||
       !aligned(a.d_s, 4))
     return MQC_E_ALIGN;
+  return MQC_OK;
+}
+
+template <typename T>
+int launch_ssm_bwd(const SsmBwdArgs& a, hipStream_t s) {
+  // T == 0 still launches: the walk is empty, dh0 = dh_last and the parameter
+  // partials are zero.
+  if (a.batch == 0 || a.Dm == 0) return MQC_OK;
+  const int chk = ssm_bwd_check<T>(a);
+  if (chk != MQC_OK) return chk;
   const int64_t S = a.S;
   if (S <= 1) return launch_ssm_bwd_g<T, 1>(a, s);
   if (S <= 2) return launch_ssm_bwd_g<T, 2>(a, s);

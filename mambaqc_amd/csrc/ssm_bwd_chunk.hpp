@@ -156,6 +156,9 @@ int launch_bwd_agg_g(const SsmBwdArgs& a, float* Hc, float* Pc, hipStream_t s) {
 template <typename T>
 int ssm_bwd_chunked_launch(const SsmBwdArgs& a0, float* ws, hipStream_t s) {
   SsmBwdArgs a = a0;
+  // The backward's own argument checks, before the carry launch reads anything.
+  const int chk = ssm_bwd_check<T>(a);
+  if (chk != MQC_OK) return chk;
   const int64_t nc = a.n_chunks - 1;
   float* Hc = ws;
   float* Pc = ws + a.batch * nc * a.Dm * a.S * 4;

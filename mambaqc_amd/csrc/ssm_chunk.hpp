@@ -346,6 +346,9 @@ int launch_carry_prefix(const SsmArgs& a, float* Hc, const float* Pc, hipStream_
 template <typename T>
 int ssm_chunk_launch(const SsmArgs& a0, float* ws, hipStream_t s) {
   SsmArgs a = a0;
+  // The walk's own argument checks, before the carry launch reads anything.
+  const int chk = ssm_check<T, MODE_DL>(a);
+  if (chk != MQC_OK) return chk;
   const int64_t nc = a.n_chunks - 1;
   float* Hc = ws;
   float* Pc = ws + a.batch * nc * a.Dm * a.S * 4;

@@ -633,11 +633,10 @@ int launch_ssm_kpl(const SsmArgs& a, hipStream_t s) {
 // per lane for 16-bit storage, one for fp32), wider lanes for d_state > 64.
 // KPL states per lane need d_state % KPL == 0 (lanes past the last k are
 // clamped onto the last KPL states).
+// What every launch of the walk needs of its arguments, checked on the host
+// before any kernel runs (the chunked walk calls it before its carry launch).
 template <typename T, int MODE>
-int launch_ssm(const SsmArgs& a, hipStream_t s) {
-  // T == 0 with h_last still launches: the walk is empty and the kernel writes
-  // h_last from h0 (or zeros).
-  if (a.batch == 0 || a.Dm == 0 || (a.T == 0 && !a.h_last)) return MQC_OK;
+int ssm_check(const SsmArgs& a) {
   // Per-(b, t) slices (and the strided D vector) are addressed with 32-bit lane
   // offsets; step counters are 32-bit.
   if (a.Dm * a.S * 4 * (int64_t)sizeof(T) >= ((int64_t)1 << 31)) return MQC_E_LIMIT;
@@ -652,6 +651,16 @@ int launch_ssm(const SsmArgs& a, hipStream_t s) {
       (MODE == MODE_Q && (!aligned(a.q, qa) || !aligned(a.Sq, qa) || !aligned(a.Dq, sizeof(T)))) ||
       (a.h0 && !aligned(a.h0, ha)) || (a.h_last && !aligned(a.h_last, ha)))
     return MQC_E_ALIGN;
+  return MQC_OK;
+}
+
+template <typename T, int MODE>
+int launch_ssm(const SsmArgs& a, hipStream_t s) {
+  // T == 0 with h_last still launches: the walk is empty and the kernel writes
+  // h_last from h0 (or zeros).
+  if (a.batch == 0 || a.Dm == 0 || (a.T == 0 && !a.h_last)) return MQC_OK;
+  const int chk = ssm_check<T, MODE>(a);
+  if (chk != MQC_OK) return chk;
   auto wide_ok = [&](int kpl) {
     const uintptr_t al = kpl * 4 * sizeof(T) >= 16 ? 16 : kpl * 4 * sizeof(T);
     const uintptr_t hal = MODE == MODE_DL ? 16 : al;

@@ -423,6 +423,33 @@ def test_torch_ops_registered_with_fake_kernels():
         mm.quaternion_multiply(torch.zeros(2, 4), torch.zeros(2, 4))
 
 
+def test_chunked_walks_check_before_any_launch():
+    """The chunked entry points run the walk's own argument checks (alignment,
+    32-bit slice offsets) before their first launch: without a GPU they return
+    the check's code, not a HIP error from a carry launch that ran first."""
+    lib = nat.load()
+    bf = 1
+    K = lib.mqc_ssm_bwd_ckpt_every(bf)
+    odd = ctypes.c_void_p(4096 + 2)  # 2-byte aligned: too little for 8-byte B loads
+    big = 1 << 40
+    # Inference: (delta, s, B, C, la, li, D, h0, y, h_last, batch, T, d, S, L, eps, dtype, ws, bytes, stream)
+    P = [FAKE, FAKE, odd] + [FAKE] * 7
+    assert lib.mqc_ssm_fused_fwd_chunked(*P, 1, 200, 8, 64, 64, 1e-6, bf, FAKE, big, None) == -4
+    P = [FAKE] * 10
+    # 2^22 d's x 64 states x 4 x 2 bytes = 2 GiB per (b, t) slice: past the 32-bit offsets.
+    assert lib.mqc_ssm_fused_fwd_chunked(*P, 1, 200, 1 << 22, 64, 64, 1e-6, bf, FAKE, big, None) == -5
+    # Training forward: 11 pointers (… h_last, h_ckpt), then ckpt_every.
+    P = [FAKE, FAKE, odd] + [FAKE] * 8
+    assert lib.mqc_ssm_fused_fwd_train_chunked(*P, K, 1, 200, 8, 64, 64, 1e-6, bf, FAKE, big, None) == -4
+    # Backward: 9 pointers, ckpt_every, 10 pointers (gy first).
+    Q = [FAKE] * 9
+    R = [odd] + [FAKE] * 9
+    assert lib.mqc_ssm_fused_bwd_chunked(*Q, K, *R, 1, 200, 8, 64, 64, 1e-6, bf, FAKE, big, None) == -4
+    R = [FAKE] * 10
+    assert lib.mqc_ssm_fused_bwd_chunked(*Q, K, *R, 1, 200, 1 << 22, 64, 64, 1e-6, bf, FAKE, big,
+                                         None) == -5
+
+
 def test_chunked_training_validation_without_gpu():
     """The chunked training entry points refuse, before any HIP call, a chunk
     length that is not a multiple of the checkpoint interval, a short
