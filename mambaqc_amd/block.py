@@ -222,9 +222,12 @@ class _SlicedBCTrain(torch.autograd.Function):
         dli = torch.empty(D, S, 3, device=dev, dtype=f32)
         dD = torch.empty(D, device=dev, dtype=f32)
         dh0 = None if h0 is None else torch.empty(b, D, S, 4, device=dev, dtype=f32)
-        dwb = torch.empty(wb.shape, device=dev, dtype=f32)
-        dwc = torch.empty(wc.shape, device=dev, dtype=f32)
-        dx2 = torch.zeros(m, D, device=dev, dtype=f32)
+        # Weight gradients and the projections' share of dx only where asked
+        # for (frozen projections skip two GEMMs per slice each).
+        need_x, need_wb, need_wc = (ctx.needs_input_grad[i] for i in (0, 3, 4))
+        dwb = torch.empty(wb.shape, device=dev, dtype=f32) if need_wb else None
+        dwc = torch.empty(wc.shape, device=dev, dtype=f32) if need_wc else None
+        dx2 = torch.zeros(m, D, device=dev, dtype=f32) if need_x else None
         buf = torch.empty(2, m * width * S * 4, device=dev, dtype=dtype)
         gy = gy if gy is not None else torch.zeros(b, t, D, 4, device=dev, dtype=dtype)
         for d0 in range(0, D, width):
@@ -248,15 +251,19 @@ class _SlicedBCTrain(torch.autograd.Function):
                 dh0[:, d0:d0 + n] = dh0_s
             dB2 = dB.view(m, n * S * 4)
             dC2 = dC.view(m, n * S * 4)
-            torch.mm(dB2.t(), x2, **wide, out=dwb[r0:r1])
-            torch.mm(dC2.t(), x2, **wide, out=dwc[r0:r1])
-            dx2.add_(torch.mm(dB2, wb.detach()[r0:r1].to(dtype), **wide))
-            dx2.add_(torch.mm(dC2, wc.detach()[r0:r1].to(dtype), **wide))
+            if need_wb:
+                torch.mm(dB2.t(), x2, **wide, out=dwb[r0:r1])
+            if need_wc:
+                torch.mm(dC2.t(), x2, **wide, out=dwc[r0:r1])
+            if need_x:
+                dx2.add_(torch.mm(dB2, wb.detach()[r0:r1].to(dtype), **wide))
+                dx2.add_(torch.mm(dC2, wc.detach()[r0:r1].to(dtype), **wide))
             del dB, dC, dB2, dC2
         d_dt, d_g, d_x = _sf._front_backward(dt, g, xv, d_delta, d_s)
-        dx = d_x.float().add_(dx2.view(b, t, D))
-        return (dx.to(x_act.dtype), d_dt.to(dt_raw.dtype), d_g.to(g_raw.dtype),
-                dwb.to(wb.dtype), dwc.to(wc.dtype), dla.to(lam_a.dtype), dli.to(lam_i.dtype),
+        dx = d_x.float().add_(dx2.view(b, t, D)).to(x_act.dtype) if need_x else None
+        return (dx, d_dt.to(dt_raw.dtype), d_g.to(g_raw.dtype),
+                None if dwb is None else dwb.to(wb.dtype),
+                None if dwc is None else dwc.to(wc.dtype), dla.to(lam_a.dtype), dli.to(lam_i.dtype),
                 dD.to(dskip.dtype), None if dh0 is None else dh0.to(h0.dtype),
                 None, None, None, None)
 

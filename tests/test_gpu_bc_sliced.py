@@ -135,6 +135,28 @@ def test_sliced_training_equals_whole(dtype, rtol, width):
         assert_close(a, b, max(rtol, 1e-4), f"sliced training grad {n} w{width}")
 
 
+def test_sliced_training_frozen_projections():
+    """B_proj and C_proj frozen: the sliced backward skips their weight
+    gradients (None, as the whole path leaves them) and the other gradients
+    still equal the whole path's."""
+    blk = _block(64, 16, torch.float32, seed=11)
+    blk.B_proj.weight.requires_grad_(False)
+    blk.C_proj.weight.requires_grad_(False)
+    g = torch.Generator(device=DEV).manual_seed(12)
+    x = torch.randn(2, 40, 64, generator=g, device=DEV)
+    gy = torch.randn(2, 40, 64, generator=g, device=DEV)
+    res = {}
+    for width in (0, 5):
+        blk.bc_slice_d = width
+        blk.zero_grad(set_to_none=True)
+        xr = x.clone().requires_grad_()
+        (blk(xr) * gy).sum().backward()
+        assert blk.B_proj.weight.grad is None and blk.C_proj.weight.grad is None
+        res[width] = [xr.grad] + [p.grad for p in blk.parameters() if p.requires_grad]
+    for a, b in zip(res[5], res[0]):
+        assert_close(a, b, 1e-4, "frozen-projection sliced grads")
+
+
 def test_sliced_training_autocast_and_state():
     """fp32 parameters under fp16 autocast (the config-4 setting) and a
     recurrent state with gradients (h0 and h_last), sliced against whole."""
