@@ -248,6 +248,13 @@ def test_block_backward_ragged():
     _block_grads_vs_oracle(24, 5, 2, (2, 19, 24), seed=4)
 
 
+def test_block_backward_headline_width():
+    """The headline configuration's width (d_model 768, d_state 64, expand 2:
+    two 604 M-parameter projections) at B1 T32: every gradient of the block
+    against fp64 autograd through the oracle."""
+    _block_grads_vs_oracle(768, 64, 2, (1, 32, 768), seed=21)
+
+
 def test_block_backward_chunked_walks():
     """Batch 1, 300 steps, 4 x 16 states: the SSM's training walk and backward
     run in time chunks (train_chunk_len < seq_len), inside the block's autograd."""
