@@ -547,12 +547,14 @@ def lm_timing(args):
     # Recurrent decoding after the 2048-token prompt: one step per new token
     # (the reference re-runs the whole sequence instead).
     # The decode step as generate() runs it: fed back tokens are sampled in
-    # range, so the step skips the id check (a host round trip per step).
+    # range, so the step skips the id check (a host round trip per step), and it
+    # updates generate()'s own copies of the states in place.
     with torch.inference_mode():
         _, states = lm.forward_with_state(ids)
         tok = ids[:, -1:]
-        lm._forward_with_state(tok, states)
-        dec_ms = event_time_ms(lambda: lm._forward_with_state(tok, states), 20)
+        st = [(tail.contiguous(), h.clone()) for tail, h in states]
+        lm._step_state_(tok, st)
+        dec_ms = event_time_ms(lambda: lm._step_state_(tok, st), 20)
     log(f"config 5 recurrent decode: {dec_ms:.2f} ms per step of {B} tokens")
     from mambaqc_amd.lm import DecodeGraph
     with torch.no_grad():
@@ -648,7 +650,8 @@ def run_kernel_loop(args):
             _, states = lm.forward_with_state(ids)
             tok = ids[:, -1:]
             if args.mode == "decode":
-                fn = lambda: lm._forward_with_state(tok, states)
+                st = [(tail.contiguous(), h.clone()) for tail, h in states]
+                fn = lambda: lm._step_state_(tok, st)
             else:
                 with torch.inference_mode(False), torch.no_grad():
                     graph = DecodeGraph(lm, states)

@@ -111,7 +111,9 @@ int mqc_ssm_q_fwd(const void* q, const void* B, const void* S, const void* C, co
  * fp32 whatever dtype is, so a walk split into pieces (recurrent decoding)
  * gives the same y as the whole walk. With seq_len 0, h_last (if given)
  * receives h0, or zeros; delta, s, B, C and y may then be NULL, the
- * parameters may not.
+ * parameters may not. h_last may be h0 (the state updated in place, as the
+ * recurrent decode does): each state is written only by the lane that read it,
+ * after its walk.
  * Replaces the body of QuaternionMamba2Block._ssm_forward,
  * mambaqc/models/quaternion_mamba2_block.py:206-228 (Lambda, z = delta*Lambda,
  * cayley_discretization_fused, ssm_forward_fused), without materialising z or q. */
@@ -225,6 +227,21 @@ int mqc_causal_conv_silu_bwd(const void* x, int64_t x_row_stride, const float* w
                              const float* bias, const void* gout, void* dx, int64_t dx_row_stride,
                              float* dw_part, float* dbias_part, int64_t batch, int64_t seq_len,
                              int64_t channels, int64_t kernel, int dtype, void* stream);
+
+/* One step of mqc_causal_conv_silu_fwd for recurrent decoding: one new row per
+ * batch row, x: dtype, element (b,c) at x[b * x_row_stride + c]; tail: dtype
+ * dense [batch, kernel-1, channels], the kernel-1 inputs before x, oldest first
+ * (may be NULL when kernel == 1). Writes out (dtype dense [batch, channels]) =
+ * silu(bias[c] + sum_{j<kernel-1} w[c,j] * tail[b,j,c] + w[c,kernel-1] * x[b,c]),
+ * the forward's value for that row with the same order of operations, and then
+ * updates tail in place to the last kernel-1 inputs including x (bit copies).
+ * The reference has no recurrent decode: its generate() reruns CausalConv1d.forward
+ * over the whole sequence for every new token (mambaqc/models/quaternion_mamba2.py:192-225,
+ * mambaqc/layers/causal_conv1d.py:68-91); this replaces the concatenation of the
+ * cached tail with the new row and that conv in the one-token step. */
+int mqc_causal_conv_silu_step(const void* x, int64_t x_row_stride, void* tail, const float* w,
+                              const float* bias, void* out, int64_t batch, int64_t channels,
+                              int64_t kernel, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Training: forward with state checkpoints, and the backward passes.

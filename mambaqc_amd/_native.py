@@ -55,6 +55,7 @@ SIGNATURES = {
     "mqc_conv_run_length": [],
     "mqc_causal_conv_silu_bwd": [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64,
                                  _i64, _i64, _int, _vp],
+    "mqc_causal_conv_silu_step": [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
     "mqc_ssm_fused_fwd_chunked": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp, _i64, _vp],
     "mqc_gemm_nt": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
@@ -76,7 +77,7 @@ SIGNATURES_I64 = {
     "mqc_ssm_chunked_scratch_bytes": [],
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib = None
@@ -182,22 +183,21 @@ def param_f32(t: torch.Tensor) -> torch.Tensor:
     model dtype). An fp32 tensor that already qualifies is used as is; other
     conversions are cached and redone when the tensor's data pointer, shape or
     version counter (bumped by every in-place update) changes. Inference
-    tensors, and any tensor while inference mode is on, are converted on every
-    call (the former have no version counter; a conversion made in inference
-    mode could not be saved for a later backward)."""
+    tensors (made in inference mode) have no version counter and are converted
+    on every call. The cached conversions are made with inference mode off,
+    also when the call comes from inside it: a conversion made in inference
+    mode would be an inference tensor, which autograd could not save if the
+    cache handed it to a later training step."""
     if t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0:
         return t.detach()
-    if t.is_inference() or torch.is_inference_mode_enabled():
-        # An inference tensor has no version counter to tell an in-place
-        # update; a conversion made in inference mode is an inference tensor,
-        # which autograd could not save if the cache handed it to a later
-        # training step. Both convert every time.
+    if t.is_inference():
         return aligned16(t.detach().float())
     key = (t._version, t.data_ptr(), t.dtype, tuple(t.shape))
     hit = _F32_CACHE.get(id(t))
     if hit is not None and hit[0]() is t and hit[1] == key:
         return hit[2]
-    conv = aligned16(t.detach().float())
+    with torch.inference_mode(False):
+        conv = aligned16(t.detach().float())
     if hit is None or hit[0]() is not t:
         weakref.finalize(t, _F32_CACHE.pop, id(t), None)
     _F32_CACHE[id(t)] = (weakref.ref(t), key, conv)

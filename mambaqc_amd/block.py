@@ -37,7 +37,7 @@ from . import _native as nat
 from .kernels.quaternion_norm import QuaternionLayerNorm
 from .kernels import ssm_fused as _sf
 from .kernels.ssm_fused import ssm_forward_front_dl, ssm_forward_fused_dl, ssm_front
-from .layers.causal_conv1d import CausalConv1d, causal_conv1d_silu
+from .layers.causal_conv1d import CausalConv1d, causal_conv1d_silu, causal_conv1d_silu_step_
 from .layers.quaternion_linear import quaternion_to_real_projection, real_to_quaternion_projection
 
 
@@ -338,6 +338,30 @@ class QuaternionMamba2Block(nn.Module):
         y, h = self._ssm_forward(x_act, h0=h0, return_state=True)
         y_real = self.out_proj(self.norm(y))
         return out_gate(x, z, y_real), (xc[:, xc.shape[1] - k:], h)
+
+    def step_state_(self, x: torch.Tensor, state) -> torch.Tensor:
+        """One token per sequence, x [batch, 1, d_model], continued from state =
+        (conv_tail, h), which is updated in place to the state after x; returns
+        out [batch, 1, d_model], equal to forward_with_state(x, state)[0]. The
+        recurrent decode step, without autograd: conv_tail contiguous
+        [batch, d_conv - 1, d_inner] in x's dtype, h contiguous fp32
+        [batch, d_inner, d_state, 4]. The conv continues from the tail in one
+        kernel that also shifts it, and the SSM writes its final state over h, so
+        the step copies no state."""
+        tail, h = state
+        xz = self.in_proj(x)
+        x_in, z = xz.chunk(2, dim=-1)
+        conv = self.conv1d.conv
+        x_act = causal_conv1d_silu_step_(x_in, tail, conv.weight, conv.bias)
+        b, t, D = x_act.shape
+        dt_raw = self.dt_proj(x_act)
+        g_raw = self.gate_proj(x_act)
+        Bq = self.B_proj(x_act).view(b, t, D, self.d_state, 4)
+        Cq = self.C_proj(x_act).view(b, t, D, self.d_state, 4)
+        y = _sf.ssm_forward_front_dl_state_(dt_raw, g_raw, x_act, Bq, Cq, self.Lambda_alpha,
+                                            self.Lambda_imag, self.D, h, eps=1e-6)
+        y_real = self.out_proj(self.norm(y))
+        return out_gate(x, z, y_real)
 
     def _ssm_forward(self, x: torch.Tensor, h0: torch.Tensor | None = None,
                      return_state: bool = False):

@@ -102,6 +102,48 @@ __global__ __launch_bounds__(kConvThreads) void conv_silu_fwd_kernel(
   }
 }
 
+// One decode step: the conv over one new row per batch row, continued from the
+// K-1 rows before it, which live in `tail` [B, K-1, C] (oldest first). Every
+// thread owns one (b, c): out[b, c] is the forward's pre-activation over the
+// window (tail rows, then x) in the same order, so a sequence fed step by step
+// equals it fed whole; then the thread shifts its column of the tail by one
+// row and appends x, as raw storage copies. Each thread reads its tail column
+// before writing it and no two threads share one, so the update is in place.
+//
+// PACK: the rounding of the forward's 16-byte path, which the forward takes for
+// whole sequences when C is a multiple of its vector width: the product
+// p * sigmoid(p) rounded to fp32, then converted with the packed conversion.
+// Without it the compiler fuses the product and the conversion to a 16-bit
+// type into one instruction (one rounding), as the forward's element path
+// does; the two can differ in the last bit of a 16-bit output.
+template <typename T, int K, bool PACK>
+__global__ __launch_bounds__(kConvThreads) void conv_silu_step_kernel(
+    const T* __restrict__ x, int64_t xs, T* tail, const float* __restrict__ w,
+    const float* __restrict__ bias, T* __restrict__ out, int64_t Bn, int64_t C) {
+  const int64_t item = (int64_t)blockIdx.x * kConvThreads + threadIdx.x;
+  if (item >= Bn * C) return;
+  const int64_t b = item / C;
+  const int64_t c = item - b * C;
+  T* tc = tail + b * (K - 1) * C + c;
+  const T xv = x[b * xs + c];
+  T raw[K];
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) raw[j] = tc[j * C];
+  raw[K - 1] = xv;
+  float p = bias ? bias[c] : 0.f;
+#pragma unroll
+  for (int j = 0; j < K; ++j) p = fmaf(w[c * K + j], io<T>::to_f32(raw[j]), p);
+  float o = p * sigmoid_f(p);
+  if constexpr (PACK && sizeof(T) == 2) {
+    asm volatile("" : "+v"(o));  // keep the product an fp32 value
+    out[b * C + c].bits = (uint16_t)(pack2<T>(o, o) & 0xffffu);
+  } else {
+    store_scalar(out + b * C + c, o);
+  }
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) tc[j * C] = raw[j + 1];
+}
+
 // Backward. Thread layout as the forward. dw_part / db_part: [Bn * runs, C, K]
 // and [Bn * runs, C] (fp32).
 template <typename T, int K, int TR, int V>
@@ -285,6 +327,42 @@ int dispatch_conv(int dtype, A... args) {
   }
 }
 
+template <typename T, int K>
+int launch_conv_step_k(const void* x, int64_t xs, void* tail, const float* w, const float* bias,
+                       void* out, int64_t Bn, int64_t C, hipStream_t s) {
+  const int64_t blocks = (Bn * C + kConvThreads - 1) / kConvThreads;
+  if (blocks > 0x7fffffffLL) return MQC_E_LIMIT;
+  // The forward's rounding for a sequence of this width (its 16-byte path
+  // applies when C is a multiple of the vector width).
+  if (C % conv_vec<T>() == 0)
+    conv_silu_step_kernel<T, K, true><<<dim3((unsigned)blocks), dim3(kConvThreads), 0, s>>>(
+        (const T*)x, xs, (T*)tail, w, bias, (T*)out, Bn, C);
+  else
+    conv_silu_step_kernel<T, K, false><<<dim3((unsigned)blocks), dim3(kConvThreads), 0, s>>>(
+        (const T*)x, xs, (T*)tail, w, bias, (T*)out, Bn, C);
+  return launch_status();
+}
+
+template <typename T>
+int launch_conv_step(const void* x, int64_t xs, void* tail, const float* w, const float* bias,
+                     void* out, int64_t Bn, int64_t C, int64_t K, hipStream_t s) {
+  if (Bn == 0 || C == 0) return MQC_OK;
+  if (!aligned(x, sizeof(T)) || !aligned(out, sizeof(T)) || !aligned(tail, sizeof(T)) ||
+      !aligned(w, 4) || (bias && !aligned(bias, 4)))
+    return MQC_E_ALIGN;
+  switch (K) {
+    case 1: return launch_conv_step_k<T, 1>(x, xs, tail, w, bias, out, Bn, C, s);
+    case 2: return launch_conv_step_k<T, 2>(x, xs, tail, w, bias, out, Bn, C, s);
+    case 3: return launch_conv_step_k<T, 3>(x, xs, tail, w, bias, out, Bn, C, s);
+    case 4: return launch_conv_step_k<T, 4>(x, xs, tail, w, bias, out, Bn, C, s);
+    case 5: return launch_conv_step_k<T, 5>(x, xs, tail, w, bias, out, Bn, C, s);
+    case 6: return launch_conv_step_k<T, 6>(x, xs, tail, w, bias, out, Bn, C, s);
+    case 7: return launch_conv_step_k<T, 7>(x, xs, tail, w, bias, out, Bn, C, s);
+    case 8: return launch_conv_step_k<T, 8>(x, xs, tail, w, bias, out, Bn, C, s);
+    default: return MQC_E_LIMIT;
+  }
+}
+
 }  // namespace mqc
 
 using namespace mqc;
@@ -318,6 +396,22 @@ int mqc_causal_conv_silu_bwd(const void* x, int64_t x_row_stride, const float* w
     return MQC_E_NULL;
   return dispatch_conv(dtype, true, x, x_row_stride, w, bias, gout, dx, dx_row_stride, dw_part,
                        dbias_part, batch, seq_len, channels, kernel, (hipStream_t)stream);
+}
+
+int mqc_causal_conv_silu_step(const void* x, int64_t x_row_stride, void* tail, const float* w,
+                              const float* bias, void* out, int64_t batch, int64_t channels,
+                              int64_t kernel, int dtype, void* stream) {
+  if (batch < 0 || channels < 0 || kernel < 1 || x_row_stride < channels) return MQC_E_SHAPE;
+  if (kernel > kConvMaxK) return MQC_E_LIMIT;
+  if (batch > 0 && channels > 0 && (!x || !w || !out || (kernel > 1 && !tail)))
+    return MQC_E_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MQC_F32: return launch_conv_step<float>(x, x_row_stride, tail, w, bias, out, batch, channels, kernel, s);
+    case MQC_BF16: return launch_conv_step<bf16_t>(x, x_row_stride, tail, w, bias, out, batch, channels, kernel, s);
+    case MQC_F16: return launch_conv_step<f16_t>(x, x_row_stride, tail, w, bias, out, batch, channels, kernel, s);
+    default: return MQC_E_DTYPE;
+  }
 }
 
 }  // extern "C"

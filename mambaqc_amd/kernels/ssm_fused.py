@@ -349,6 +349,34 @@ def _dl_ops(delta, s, B, C, lambda_alpha, lambda_imag, D, h0, eps, return_state,
     return (y, h_last) if return_state else y
 
 
+def ssm_forward_front_dl_state_(dt_raw: torch.Tensor, g_raw: torch.Tensor, x: torch.Tensor,
+                                B: torch.Tensor, C: torch.Tensor, lambda_alpha: torch.Tensor,
+                                lambda_imag: torch.Tensor, D: torch.Tensor, h: torch.Tensor,
+                                eps: float = 1e-6) -> torch.Tensor:
+    """ssm_forward_front_dl continued from the state h, which is overwritten
+    with the final state; returns y. For the recurrent decode step (no autograd):
+    h is fp32 [batch, d_inner, d_state, 4], contiguous, and is both the kernel's
+    h0 and its h_last (one whole walk, in which each state is written only by the
+    lane that read it)."""
+    if torch.is_grad_enabled() and any(
+            t.requires_grad for t in (dt_raw, g_raw, x, B, C, lambda_alpha, lambda_imag, D, h)):
+        raise RuntimeError("ssm_forward_front_dl_state_: updates its state in place; "
+                           "run under torch.no_grad")
+    if h.dtype != torch.float32 or not h.is_contiguous() or h.data_ptr() % 16:
+        raise ValueError("ssm_forward_front_dl_state_: h must be a contiguous, 16-byte "
+                         "aligned fp32 [batch, d_inner, d_state, 4] tensor")
+    delta, s = ssm_front(dt_raw, g_raw, x)
+    batch, T, d_inner, d_state = _dl_check(delta, s, B, C, lambda_alpha, lambda_imag, D, h)
+    dl, sv, Bc, Cc, la, li, Dv, _ = _dl_operands(delta, s, B, C, lambda_alpha, lambda_imag, D,
+                                                 None)
+    y = torch.empty(batch, T, d_inner, 4, device=Bc.device, dtype=Bc.dtype)
+    nat.call("mqc_ssm_fused_fwd", Bc, dl.data_ptr(), sv.data_ptr(), Bc.data_ptr(), Cc.data_ptr(),
+             la.data_ptr(), li.data_ptr(), Dv.data_ptr(), h.data_ptr(), y.data_ptr(),
+             h.data_ptr(), batch, T, d_inner, d_state, float(eps), nat.dtype_code(Bc),
+             nat.stream_of(Bc))
+    return y
+
+
 def _front_operands(dt_raw, g_raw, x):
     if not (dt_raw.shape == g_raw.shape == x.shape):
         raise ValueError(f"ssm_front: shapes differ {tuple(dt_raw.shape)}, "

@@ -104,3 +104,29 @@ def causal_conv1d_silu(x: torch.Tensor, weight: torch.Tensor,
         return torch.ops.mambaqc.causal_conv1d_silu(x, weight, bias)
     nat.require_device("causal_conv1d_silu", x, weight)
     return _ConvSiLU.apply(x, weight, bias)
+
+
+def causal_conv1d_silu_step_(x: torch.Tensor, tail: torch.Tensor, weight: torch.Tensor,
+                             bias: torch.Tensor | None) -> torch.Tensor:
+    """One recurrent step of causal_conv1d_silu: x [batch, 1, channels] (may be
+    the strided first half of in_proj's output), tail [batch, k - 1, channels]
+    contiguous in x's dtype, the k - 1 inputs before x (oldest first). Returns
+    silu(conv) for the new row, [batch, 1, channels], equal to
+    causal_conv1d_silu(cat(tail, x))[:, -1:], and updates tail in place to the
+    last k - 1 inputs including x. No autograd (the decode step)."""
+    B, T, C = x.shape
+    K = weight.shape[-1]
+    if T != 1 or weight.shape[0] != C:
+        raise ValueError(f"causal_conv1d_silu_step_: x must be [batch, 1, {weight.shape[0]}], "
+                         f"got {tuple(x.shape)}")
+    if tail.shape != (B, K - 1, C) or tail.dtype != x.dtype or not tail.is_contiguous():
+        raise ValueError(f"causal_conv1d_silu_step_: tail must be a contiguous {x.dtype} "
+                         f"[{B}, {K - 1}, {C}] tensor, got {tuple(tail.shape)} {tail.dtype}")
+    nat.require_device("causal_conv1d_silu_step_", x, tail, weight)
+    xv, xs = _rows_view(x.detach())
+    w = nat.param_f32(weight).reshape(C, K)
+    b = None if bias is None else nat.param_f32(bias)
+    out = torch.empty(B, 1, C, device=x.device, dtype=x.dtype)
+    nat.call("mqc_causal_conv_silu_step", xv, xv.data_ptr(), xs, tail.data_ptr(), w.data_ptr(),
+             nat.ptr(b), out.data_ptr(), B, C, K, nat.dtype_code(xv), nat.stream_of(xv))
+    return out

@@ -109,6 +109,16 @@ class QuaternionMamba2(nn.Module):
             new_states.append(st)
         return self._head(x), new_states
 
+    def _step_state_(self, input_ids: torch.Tensor, states) -> torch.Tensor:
+        """Logits [batch, 1, vocab] of one token per sequence continued from the
+        per-layer states, which are updated in place (QuaternionMamba2Block.step_state_:
+        contiguous conv tails in the model's dtype, fp32 SSM states). No id check,
+        as in _forward_with_state."""
+        x = self.dropout(self.embedding(input_ids))
+        for layer, st in zip(self.layers, states):
+            x = layer.step_state_(x, st)
+        return self._head(x)
+
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 100,
                  temperature: float = 1.0, top_k: int | None = None,
@@ -125,6 +135,9 @@ class QuaternionMamba2(nn.Module):
             return input_ids
         logits, states = self.forward_with_state(input_ids)
         graph = DecodeGraph(self, states) if use_graph and max_new_tokens > 1 else None
+        # The decode steps update these states in place (contiguous tails: the
+        # prompt's are views of its last rows).
+        states = [(tail.contiguous(), h) for tail, h in states]
         for step in range(max_new_tokens):
             nxt = logits[:, -1, :] / temperature
             if top_k is not None:
@@ -144,7 +157,7 @@ class QuaternionMamba2(nn.Module):
                 if graph is not None:
                     logits = graph.step(token)
                 else:
-                    logits, states = self._forward_with_state(token, states)
+                    logits = self._step_state_(token, states)
         return input_ids
 
     def get_num_params(self, non_embedding: bool = True) -> int:
@@ -164,8 +177,9 @@ class DecodeGraph:
     step's ~12 kernels per layer would otherwise each be launched from Python.
 
     The graph reads its tokens and the per-layer states (conv tails, fp32 SSM
-    states) from static buffers and writes the new states back into them, so
-    each replay advances the sequences by one token: step(tokens) copies the
+    states) from static buffers and its kernels update those states in place
+    (QuaternionMamba2Block.step_state_), so each replay advances the sequences
+    by one token: step(tokens) copies the
     tokens in, replays, and returns the static logits buffer [batch, 1, vocab]
     (valid until the next step). Built from the states a prompt's
     forward_with_state returned (they are copied; the caller's stay as they
@@ -184,7 +198,9 @@ class DecodeGraph:
         batch = states[0][1].shape[0]
         self.lm = lm
         self.tokens = torch.zeros(batch, 1, dtype=torch.long, device=dev)
-        self.states = [(tail.detach().clone(), h.detach().clone()) for tail, h in states]
+        self.states = [(tail.detach().clone(memory_format=torch.contiguous_format),
+                        h.detach().clone(memory_format=torch.contiguous_format))
+                       for tail, h in states]
         saved = [(tail.clone(), h.clone()) for tail, h in self.states]
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
@@ -200,11 +216,7 @@ class DecodeGraph:
             h.copy_(h0)
 
     def _step(self) -> torch.Tensor:
-        logits, new = self.lm._forward_with_state(self.tokens, self.states)
-        for (tail, h), (nt, nh) in zip(self.states, new):
-            tail.copy_(nt)
-            h.copy_(nh)
-        return logits
+        return self.lm._step_state_(self.tokens, self.states)
 
     def step(self, tokens: torch.Tensor) -> torch.Tensor:
         self.tokens.copy_(tokens)

@@ -349,8 +349,8 @@ def test_ssm_empty_sequence(dtype):
 
 def test_training_after_inference_mode():
     """A bf16 block run under torch.inference_mode, then trained: the library's
-    fp32 copies of its small parameters made in inference mode are not reused
-    by the training step (autograd could not save them)."""
+    fp32 copies of its small parameters, converted during inference mode, are
+    ordinary tensors that the training step can save for its backward."""
     torch.manual_seed(8)
     blk = mambaqc_amd.QuaternionMamba2Block(32, d_state=8).to(DEV, torch.bfloat16)
     x = torch.randn(2, 30, 32, device=DEV).to(torch.bfloat16)

@@ -29,7 +29,7 @@ def declared_symbols():
 
 def test_header_declares_the_api():
     names = declared_symbols()
-    assert len(names) == 30, names
+    assert len(names) == 31, names
     assert set(nat.SIGNATURES) | set(nat.SIGNATURES_I64) <= set(names)
 
 
@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     lib = nat.load()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mqc_abi_version() == nat.ABI_VERSION == 4
+    assert lib.mqc_abi_version() == nat.ABI_VERSION == 5
 
 
 def test_status_strings():
@@ -421,6 +421,41 @@ def test_torch_ops_registered_with_fake_kernels():
     assert sh(mm.out_gate(m(2, 5, 8), m(2, 5, 16, dt=bf), m(2, 5, 8, dt=bf))) == [((2, 5, 8), torch.float32)]
     with pytest.raises(RuntimeError):
         mm.quaternion_multiply(torch.zeros(2, 4), torch.zeros(2, 4))
+
+
+def test_param_f32_cache_under_inference_mode():
+    """fp32 copies of 16-bit parameters are cached also when the call comes
+    from inference mode (made as ordinary tensors), and redone after an
+    in-place update; tensors made in inference mode convert every time."""
+    p = torch.nn.Parameter(torch.randn(8, 3).to(torch.bfloat16))
+    with torch.inference_mode():
+        a = nat.param_f32(p)
+        b = nat.param_f32(p)
+    assert a is b and not a.is_inference() and a.dtype == torch.float32
+    assert torch.equal(a, p.detach().float())
+    with torch.no_grad():
+        p.add_(1)
+    c = nat.param_f32(p)
+    assert c is not a and torch.equal(c, p.detach().float())
+    with torch.inference_mode():
+        t = torch.randn(4).to(torch.bfloat16)
+        assert nat.param_f32(t) is not nat.param_f32(t)
+
+
+def test_conv_step_validation_without_gpu():
+    """mqc_causal_conv_silu_step refuses bad sizes, NULLs and misaligned
+    pointers before any HIP call."""
+    lib = nat.load()
+    bf = 1
+    odd = ctypes.c_void_p(4096 + 1)
+    # (x, x_row_stride, tail, w, bias, out, batch, channels, kernel, dtype, stream)
+    assert lib.mqc_causal_conv_silu_step(FAKE, 16, FAKE, FAKE, None, FAKE, 2, 16, 0, bf, None) == -2
+    assert lib.mqc_causal_conv_silu_step(FAKE, 8, FAKE, FAKE, None, FAKE, 2, 16, 4, bf, None) == -2
+    assert lib.mqc_causal_conv_silu_step(FAKE, 16, FAKE, FAKE, None, FAKE, 2, 16, 9, bf, None) == -5
+    assert lib.mqc_causal_conv_silu_step(FAKE, 16, None, FAKE, None, FAKE, 2, 16, 4, bf, None) == -1
+    assert lib.mqc_causal_conv_silu_step(FAKE, 16, FAKE, FAKE, None, FAKE, 2, 16, 4, 7, None) == -3
+    assert lib.mqc_causal_conv_silu_step(odd, 16, FAKE, FAKE, None, FAKE, 2, 16, 4, bf, None) == -4
+    assert lib.mqc_causal_conv_silu_step(None, 16, None, None, None, None, 0, 16, 4, bf, None) == 0
 
 
 def test_chunked_walks_check_before_any_launch():
