@@ -189,6 +189,19 @@ int64_t mqc_ssm_chunked_scratch_bytes(void);
 int mqc_gemm_nt(const void* X, const void* W, void* C, int64_t M, int64_t N, int64_t K, int dtype,
                 void* stream);
 
+/* Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]) for few rows (M <= 16, a decode
+ * step's tokens), dtype MQC_BF16 or MQC_F16, fp32 accumulation: the F.linear of
+ * an nn.Linear / QuaternionLinear (mambaqc/layers/quaternion_linear.py:145-172;
+ * the block's layers, mambaqc/models/quaternion_mamba2_block.py:78-122) in the
+ * recurrent decode. A second weight sharing X (W2, bias2, Y2, N2 > 0) runs in
+ * the same launch; N2 = 0 for one. X dense [M, K], 16-byte aligned; W1, W2
+ * dense [N, K], 16-byte aligned; bias1, bias2 dtype [N] or NULL; Y1, Y2 dense
+ * [M, N]. K must be a positive multiple of 32 with M * (K + 8) * 2 <= 65536
+ * (MQC_E_LIMIT otherwise: the caller uses another GEMM). */
+int mqc_gemm_skinny_nt(const void* X, int64_t M, int64_t K, const void* W1, const void* bias1,
+                       void* Y1, int64_t N1, const void* W2, const void* bias2, void* Y2,
+                       int64_t N2, int dtype, void* stream);
+
 /* Quaternion LayerNorm over the d axis of each of `rows` rows of d quaternions:
  *   n = sqrt(|q|^2 + eps); mu, var = mean and biased variance of n over d;
  *   out = gamma * (n - mu) / sqrt(var + eps) * q / (n + eps) + beta.

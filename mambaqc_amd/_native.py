@@ -59,6 +59,7 @@ SIGNATURES = {
     "mqc_ssm_fused_fwd_chunked": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp, _i64, _vp],
     "mqc_gemm_nt": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
+    "mqc_gemm_skinny_nt": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _int, _vp],
     "mqc_ssm_fused_fwd_train_chunked": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                         _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp,
                                         _i64, _vp],

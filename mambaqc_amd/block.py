@@ -38,7 +38,8 @@ from .kernels.quaternion_norm import QuaternionLayerNorm
 from .kernels import ssm_fused as _sf
 from .kernels.ssm_fused import ssm_forward_front_dl, ssm_forward_fused_dl, ssm_front
 from .layers.causal_conv1d import CausalConv1d, causal_conv1d_silu, causal_conv1d_silu_step_
-from .layers.quaternion_linear import quaternion_to_real_projection, real_to_quaternion_projection
+from .layers.quaternion_linear import (quaternion_to_real_projection, real_to_quaternion_projection,
+                                      skinny_eligible, skinny_linear)
 
 
 def _gate_operands(x, z, y_real):
@@ -144,6 +145,41 @@ def bc_slice_width(batch: int, seq_len: int, d_inner: int, d_state: int, elsize:
         budget = BC_SLICE_BYTES
     per_d = 2 * batch * seq_len * d_state * 4 * elsize
     return max(1, min(d_inner, budget // max(per_d, 1)))
+
+
+def _linear(layer: nn.Linear, x: torch.Tensor) -> torch.Tensor:
+    """layer(x), on the library's skinny GEMM for decode-sized inputs."""
+    if skinny_eligible(x, layer.weight, layer.bias):
+        return skinny_linear(x, layer.weight, layer.bias)
+    return layer(x)
+
+
+def _linear_pair(a: nn.Linear, b: nn.Linear, x: torch.Tensor):
+    """(a(x), b(x)), in one skinny launch for decode-sized inputs."""
+    if skinny_eligible(x, a.weight, a.bias, b.weight, b.bias):
+        return skinny_linear(x, a.weight, a.bias, b.weight, b.bias)
+    return a(x), b(x)
+
+
+def _bc_pair(bp, cp, x: torch.Tensor, d_state: int):
+    """B_proj(x), C_proj(x) as [b, t, d, d_state, 4] (real -> quaternion maps),
+    in one skinny launch for decode-sized inputs with weights small enough."""
+    b, t, D = x.shape
+    bb = None if bp.bias is None else bp.bias.reshape(-1)
+    cb = None if cp.bias is None else cp.bias.reshape(-1)
+    if skinny_eligible(x, bp.weight, bb, cp.weight, cb):
+        Bq, Cq = skinny_linear(x, bp.weight, bb, cp.weight, cb)
+    else:
+        Bq, Cq = bp(x), cp(x)
+    return Bq.view(b, t, D, d_state, 4), Cq.view(b, t, D, d_state, 4)
+
+
+def _out_proj(op, y: torch.Tensor) -> torch.Tensor:
+    """out_proj(y) (quaternion -> real), on the skinny GEMM for decode-sized inputs."""
+    y2 = y.reshape(*y.shape[:-2], y.shape[-2] * 4)
+    if skinny_eligible(y2, op.weight, op.bias):
+        return skinny_linear(y2, op.weight, op.bias)
+    return op(y)
 
 
 class _SlicedBCTrain(torch.autograd.Function):
@@ -303,13 +339,13 @@ class QuaternionMamba2Block(nn.Module):
         self.bc_slice_d: int | None = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        xz = self.in_proj(x)
+        xz = _linear(self.in_proj, x)
         x_in, z = xz.chunk(2, dim=-1)
         conv = self.conv1d.conv
         x_act = causal_conv1d_silu(x_in, conv.weight, conv.bias)
         y = self._ssm_forward(x_act)
         y = self.norm(y)
-        y_real = self.out_proj(y)
+        y_real = _out_proj(self.out_proj, y)
         return out_gate(x, z, y_real)
 
     def forward_with_state(self, x: torch.Tensor, state=None):
@@ -322,7 +358,7 @@ class QuaternionMamba2Block(nn.Module):
         Feeding a sequence in pieces gives the same outputs as feeding it whole
         (up to rounding), which is what recurrent decoding relies on.
         """
-        xz = self.in_proj(x)
+        xz = _linear(self.in_proj, x)
         x_in, z = xz.chunk(2, dim=-1)
         b, _, D = x_in.shape
         k = self.d_conv - 1
@@ -336,7 +372,7 @@ class QuaternionMamba2Block(nn.Module):
         # are the continued convolution.
         x_act = causal_conv1d_silu(xc, conv.weight, conv.bias)[:, k:].contiguous()
         y, h = self._ssm_forward(x_act, h0=h0, return_state=True)
-        y_real = self.out_proj(self.norm(y))
+        y_real = _out_proj(self.out_proj, self.norm(y))
         return out_gate(x, z, y_real), (xc[:, xc.shape[1] - k:], h)
 
     def step_state_(self, x: torch.Tensor, state) -> torch.Tensor:
@@ -349,18 +385,15 @@ class QuaternionMamba2Block(nn.Module):
         kernel that also shifts it, and the SSM writes its final state over h, so
         the step copies no state."""
         tail, h = state
-        xz = self.in_proj(x)
+        xz = _linear(self.in_proj, x)
         x_in, z = xz.chunk(2, dim=-1)
         conv = self.conv1d.conv
         x_act = causal_conv1d_silu_step_(x_in, tail, conv.weight, conv.bias)
-        b, t, D = x_act.shape
-        dt_raw = self.dt_proj(x_act)
-        g_raw = self.gate_proj(x_act)
-        Bq = self.B_proj(x_act).view(b, t, D, self.d_state, 4)
-        Cq = self.C_proj(x_act).view(b, t, D, self.d_state, 4)
+        dt_raw, g_raw = _linear_pair(self.dt_proj, self.gate_proj, x_act)
+        Bq, Cq = _bc_pair(self.B_proj, self.C_proj, x_act, self.d_state)
         y = _sf.ssm_forward_front_dl_state_(dt_raw, g_raw, x_act, Bq, Cq, self.Lambda_alpha,
                                             self.Lambda_imag, self.D, h, eps=1e-6)
-        y_real = self.out_proj(self.norm(y))
+        y_real = _out_proj(self.out_proj, self.norm(y))
         return out_gate(x, z, y_real)
 
     def _ssm_forward(self, x: torch.Tensor, h0: torch.Tensor | None = None,
@@ -371,8 +404,7 @@ class QuaternionMamba2Block(nn.Module):
             x.requires_grad or (h0 is not None and h0.requires_grad)
             or any(p.requires_grad for p in self.parameters()))
         width = self._bc_slice_width(x, recording)
-        dt_raw = self.dt_proj(x)
-        g_raw = self.gate_proj(x)
+        dt_raw, g_raw = _linear_pair(self.dt_proj, self.gate_proj, x)
         if width:
             if recording:
                 if self.B_proj.bias is not None or self.C_proj.bias is not None:
@@ -383,8 +415,7 @@ class QuaternionMamba2Block(nn.Module):
                     self.Lambda_imag, self.D, h0, width, self.d_state, 1e-6, self._gemm_dtype(x))
                 return (y, h) if return_state else y
             return self._ssm_forward_sliced(x, dt_raw, g_raw, width, h0, return_state)
-        Bq = self.B_proj(x).view(b, t, D, self.d_state, 4)
-        Cq = self.C_proj(x).view(b, t, D, self.d_state, 4)
+        Bq, Cq = _bc_pair(self.B_proj, self.C_proj, x, self.d_state)
         return ssm_forward_front_dl(dt_raw, g_raw, x, Bq, Cq, self.Lambda_alpha,
                                     self.Lambda_imag, self.D, eps=1e-6, h0=h0,
                                     return_state=return_state)

@@ -16,6 +16,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .. import _native as nat
+
 _KINDS = ("real", "quaternion")
 
 # Bound on the weight bytes one GEMM launch streams in wide_linear. MI355X's
@@ -129,6 +131,61 @@ def wide_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
         out = torch.empty(*x.shape[:-1], n, device=x.device, dtype=x.dtype)
         _wide_forward(x2, weight, out.view(-1, n))
         return out
+
+
+# Decode-sized products (at most this many token rows, no autograd, 16-bit)
+# run on the library's skinny GEMM (mqc_gemm_skinny_nt), which takes a pair of
+# weights sharing the input in one launch. Measured at 4 rows on MI355X: a pair
+# of [1024 x 1024] weights 6.3 us in one launch against about 6.6 us per weight
+# through hipBLASLt, [131072 x 1024] pairs 95-98 against 99.7 us.
+SKINNY_MAX_ROWS = 16
+# Larger weights stream faster through hipBLASLt's GEMV: the base preset's
+# [393216 x 1536] B/C pair took 420 us in one skinny launch against 409 us.
+SKINNY_MAX_WEIGHT_BYTES = 512 << 20
+
+
+def skinny_eligible(x: torch.Tensor, *params) -> bool:
+    """Whether F.linear(x, w, b) for every (w, b) in params (flat: w1, b1, w2,
+    b2, ...) may run on mqc_gemm_skinny_nt: few rows, 16-bit operands of one
+    dtype, K a multiple of 32, dense weights of at most SKINNY_MAX_WEIGHT_BYTES,
+    nothing recording autograd, no autocast, not under torch.compile."""
+    if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float16) or x.dim() < 1:
+        return False
+    K = x.shape[-1]
+    rows = x.numel() // K if K else 0
+    if not (0 < rows <= SKINNY_MAX_ROWS) or K % 32 or rows * (K + 8) * 2 > (64 << 10):
+        return False
+    if torch.compiler.is_compiling() or torch.is_autocast_enabled(x.device.type):
+        return False
+    tensors = [x] + [p for p in params if p is not None]
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+        return False
+    for w, b in zip(params[0::2], params[1::2]):
+        if (w.dtype != x.dtype or w.device != x.device or w.dim() != 2 or w.shape[1] != K
+                or not w.is_contiguous() or w.data_ptr() % 16
+                or w.numel() * 2 > SKINNY_MAX_WEIGHT_BYTES):
+            return False
+        if b is not None and (b.dtype != x.dtype or b.numel() != w.shape[0]
+                              or not b.is_contiguous()):
+            return False
+    return True
+
+
+def skinny_linear(x: torch.Tensor, w1: torch.Tensor, b1: torch.Tensor | None = None,
+                  w2: torch.Tensor | None = None, b2: torch.Tensor | None = None):
+    """F.linear(x, w1, b1) and, with w2, F.linear(x, w2, b2) in one launch of
+    mqc_gemm_skinny_nt; for inputs skinny_eligible accepts. Returns y1 or
+    (y1, y2), [..., N] in x's dtype (bias added in fp32 before the rounding)."""
+    K = x.shape[-1]
+    x2 = nat.aligned16(x.reshape(-1, K))
+    M = x2.shape[0]
+    lead = x.shape[:-1]
+    y1 = torch.empty(*lead, w1.shape[0], device=x.device, dtype=x.dtype)
+    y2 = None if w2 is None else torch.empty(*lead, w2.shape[0], device=x.device, dtype=x.dtype)
+    nat.call("mqc_gemm_skinny_nt", x2, x2.data_ptr(), M, K, w1.data_ptr(), nat.ptr(b1),
+             y1.data_ptr(), w1.shape[0], nat.ptr(w2), nat.ptr(b2), nat.ptr(y2),
+             0 if w2 is None else w2.shape[0], nat.dtype_code(x2), nat.stream_of(x2))
+    return y1 if w2 is None else (y1, y2)
 
 
 class QuaternionLinear(nn.Module):

@@ -29,7 +29,7 @@ def declared_symbols():
 
 def test_header_declares_the_api():
     names = declared_symbols()
-    assert len(names) == 31, names
+    assert len(names) == 32, names
     assert set(nat.SIGNATURES) | set(nat.SIGNATURES_I64) <= set(names)
 
 
@@ -440,6 +440,25 @@ def test_param_f32_cache_under_inference_mode():
     with torch.inference_mode():
         t = torch.randn(4).to(torch.bfloat16)
         assert nat.param_f32(t) is not nat.param_f32(t)
+
+
+def test_skinny_gemm_validation_without_gpu():
+    """mqc_gemm_skinny_nt refuses bad sizes, dtypes, NULLs and misaligned
+    pointers before any HIP call."""
+    lib = nat.load()
+    bf = 1
+    odd = ctypes.c_void_p(4096 + 8)
+    # (X, M, K, W1, bias1, Y1, N1, W2, bias2, Y2, N2, dtype, stream)
+    assert lib.mqc_gemm_skinny_nt(FAKE, 17, 64, FAKE, None, FAKE, 8, None, None, None, 0, bf, None) == -5
+    assert lib.mqc_gemm_skinny_nt(FAKE, 4, 48, FAKE, None, FAKE, 8, None, None, None, 0, bf, None) == -5
+    assert lib.mqc_gemm_skinny_nt(FAKE, 4, 0, FAKE, None, FAKE, 8, None, None, None, 0, bf, None) == -5
+    assert lib.mqc_gemm_skinny_nt(FAKE, 16, 4096, FAKE, None, FAKE, 8, None, None, None, 0, bf, None) == -5
+    assert lib.mqc_gemm_skinny_nt(FAKE, 4, 64, FAKE, None, FAKE, 8, None, None, None, 0, 0, None) == -3
+    assert lib.mqc_gemm_skinny_nt(FAKE, 4, 64, None, None, FAKE, 8, None, None, None, 0, bf, None) == -1
+    assert lib.mqc_gemm_skinny_nt(FAKE, 4, 64, FAKE, None, FAKE, 8, FAKE, None, None, 8, bf, None) == -1
+    assert lib.mqc_gemm_skinny_nt(odd, 4, 64, FAKE, None, FAKE, 8, None, None, None, 0, bf, None) == -4
+    assert lib.mqc_gemm_skinny_nt(FAKE, -1, 64, FAKE, None, FAKE, 8, None, None, None, 0, bf, None) == -2
+    assert lib.mqc_gemm_skinny_nt(None, 0, 64, None, None, None, 8, None, None, None, 0, bf, None) == 0
 
 
 def test_conv_step_validation_without_gpu():
