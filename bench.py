@@ -13,6 +13,8 @@ accumulation in the HIP kernels, synthetic x ~ N(0, 1) resident in HBM.
 timed region bracketed by torch.cuda.synchronize()). `roofline` is the fused
 SSM kernel (mqc_ssm_fused_fwd): algorithmic bytes per launch divided by its
 mean launch duration, measured with HIP events on the stream it runs on.
+`roofline_gemm` puts the B projection GEMM (hipBLASLt, most of the block's
+time) against the dense bf16 MFMA peak, with this library's GEMM beside it.
 `cpu_baseline` times the CPU oracle (a restatement of the reference's
 sequential torch path) on a bounded prefix of the same workload. `train_c4`
 reports config 4 (block forward + backward under fp16 autocast) and the SSM's
@@ -36,6 +38,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "block fwd tokens/s @B4 T2048 d768 s64; scan HBM GB/s as % of peak"
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 B, T, DM, DS, DCONV, EXPAND = 4, 2048, 768, 64, 4, 2
 DI = DM * EXPAND
 
@@ -310,6 +313,7 @@ def run_full(args):
         stages["block forward, B/C in slices of 96 d's"] = event_time_ms(lambda: blk(x), 3)
         blk.bc_slice_d = None
     qln_gbs = qln_bytes(B * T, DI) / (stages["qln"] * 1e-3) / 1e9
+    gemm_flop = 2 * B * T * DI * DI * DS * 4
     del delta, s, Bq, Cq
     torch.cuda.empty_cache()
     log(f"box calibration: 1 GiB device copy {copy_gbs:.0f} GB/s; fused SSM at "
@@ -371,6 +375,21 @@ def run_full(args):
             "mean_launch_ms": round(ssm_ms, 4),
             "box_copy_GBs": round(copy_gbs, 1),
             "frac_of_box_copy": round(achieved / copy_gbs, 4),
+        },
+        # The block's time is mostly the B/C projections (hipBLASLt): their
+        # MFMA roofline beside the SSM's HBM one, with this library's GEMM.
+        "roofline_gemm": {
+            "kernel": "B_proj GEMM (hipBLASLt in column blocks, the block's path)",
+            "bound": "mfma",
+            "achieved": round(gemm_flop / (stages["B_proj GEMM hipBLASLt (column blocks)"] * 1e-3) / 1e12, 1),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_flop / (stages["B_proj GEMM hipBLASLt (column blocks)"] * 1e-3) / 1e12
+                          / PEAK_BF16_TFLOPS, 4),
+            "flop": gemm_flop,
+            "mean_launch_ms": round(stages["B_proj GEMM hipBLASLt (column blocks)"], 4),
+            "mqc_gemm_nt_TFLOPs": round(
+                gemm_flop / (stages["B_proj GEMM mqc_gemm_nt (MFMA, this library)"] * 1e-3) / 1e12, 1),
         },
         "stages_ms": {k: round(v, 4) for k, v in stages.items()},
         "components": {
