@@ -578,22 +578,27 @@ def test_wide_linear_column_blocks(monkeypatch, dtype, n):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_wide_linear_backward(monkeypatch, dtype):
+@pytest.mark.parametrize("n", [777, 769, 4096])
+def test_wide_linear_backward(monkeypatch, dtype, n):
     """Gradients of the blocked GEMMs (row-block dW, K-block dx with fp32
-    partials) against fp64 products, with ragged blocks."""
+    partials) against fp64 products, with ragged blocks: dx from one batched
+    GEMM over equal row blocks where a block count divides n (777: 21 blocks
+    of 37 rows; 4096: 16 of 256), from one GEMM per block where none does
+    (769, a prime)."""
     from mambaqc_amd.layers import quaternion_linear as ql
 
     monkeypatch.setattr(ql, "WIDE_LINEAR_CHUNK_BYTES", 16 << 10)
     monkeypatch.setattr(ql, "WIDE_LINEAR_MIN_ROWS", 1)
     x = rnd(2, 9, 96, seed=5, dtype=dtype).to(DEV).requires_grad_()
-    w = rnd(777, 96, seed=6, dtype=dtype, scale=0.1).to(DEV).requires_grad_()
-    gy = rnd(2, 9, 777, seed=7, dtype=dtype).to(DEV)
+    w = rnd(n, 96, seed=6, dtype=dtype, scale=0.1).to(DEV).requires_grad_()
+    gy = rnd(2, 9, n, seed=7, dtype=dtype).to(DEV)
     y = ql.wide_linear(x, w)
-    assert y.grad_fn is not None and len(ql._blocks(777, 96, w.element_size())) > 1
+    assert y.grad_fn is not None and len(ql._blocks(n, 96, w.element_size())) > 1
+    assert (ql._dx_batches(n, 96, w.element_size()) > 0) == (n != 769)
     y.backward(gy)
     assert_close(y, up(x) @ up(w).t(), tol(dtype), "y")
     assert_close(x.grad, up(gy) @ up(w), tol(dtype), "dx")
-    assert_close(w.grad, up(gy).reshape(-1, 777).t() @ up(x).reshape(-1, 96), tol(dtype), "dW")
+    assert_close(w.grad, up(gy).reshape(-1, n).t() @ up(x).reshape(-1, 96), tol(dtype), "dW")
 
 
 def test_wide_linear_autocast_matches_f_linear(monkeypatch):

@@ -346,6 +346,21 @@ def test_build_rejects_kernels_that_spill():
     assert B.RESOURCE_REMARKS == "-Rpass-analysis=kernel-resource-usage"
 
 
+def test_wide_linear_block_rules():
+    """Row blocks of the wide projections without a GPU: six 192 MiB blocks
+    for a config-3 B/C weight in the forward, eight equal blocks for its
+    batched input gradient (twelve for an fp32 weight), and no batched form
+    when no count from the first candidate to four times it divides the rows."""
+    from mambaqc_amd.layers import quaternion_linear as ql
+    blocks = ql._blocks(393216, 1536, 2)
+    assert len(blocks) == 6 and all(b - a == 65536 for a, b in blocks)
+    assert ql._dx_batches(393216, 1536, 2) == 8
+    assert ql._dx_batches(393216, 1536, 4) == 12
+    assert ql._dx_batches(97, 1536, 2) == 0       # a prime row count
+    assert ql._dx_batches(4 * 97, 1536, 2) == 0   # no count in 8..32 divides 388
+    assert ql._dx_batches(8 * 97, 1536, 2) == 8
+
+
 def test_bc_slice_rule():
     """The sliced B/C rule without a GPU: widths from the byte budget, whole
     projections below the bound, forced widths, and training slices refused
