@@ -24,13 +24,26 @@
 // Weights with few rows would leave most CUs idle with one wave per tile, so
 // then 4, 8 or 16 waves share each tile's K (see skinny_launch).
 //
+// Weights with many rows, at most 8 token rows and K a multiple of 64 take the
+// wide mode instead (skinny_wide_kernel): a tile reads each weight row as 64
+// bytes per instruction (half a 128-byte line), while the wide mode's load
+// instructions read 8 whole lines each and keep all of a row group's lines in
+// flight; its products run on the VALU as dot2 instructions.
+//
 // Measured on MI355X at 4 rows (bf16): a pair of [1024 x 1024] weights in one
 // launch 6.3 us, where hipBLASLt takes about 6.6 us per weight; [131072 x 1024]
-// pairs (the small preset's B/C) 95-98 us against 99.7 us for two calls; the
-// base preset's [393216 x 1536] pair 420 us against 409 us, so callers keep
-// hipBLASLt for weights that large. With every other projection of the decode
-// step here, same-box steps of 4 tokens: base preset 5.89 -> 5.72 ms eager and
-// 5.88 -> 5.70 ms as a HIP graph; small preset 2.05 -> 1.37 ms and 1.27 -> 1.09 ms.
+// pairs (the small preset's B/C) 95-98 us in tiles against 99.7 us for two
+// calls. The wide mode, same box, pairs at 4 rows unless noted, against tiles
+// and hipBLASLt: [131072 x 1024] 87-90 / 100-102 / 114-115 us; the base
+// preset's [393216 x 1536] 386-392 / 424-425 / 427 us (6.2 TB/s), at 1 row
+// 369-371 / 414-419 / 436, at 8 rows 415-416 / 455-457 / 452-458;
+// [524288 x 2048] 688-690 / 746 / 878-888 us. Decode steps of 4 tokens with
+// every projection here: base preset 5.73 -> 5.30 ms eager and 5.68-5.73 ->
+// 5.29-5.30 ms as a HIP graph against the B/C pair on hipBLASLt (same box;
+// earlier, moving the other projections here took 5.89 -> 5.72 ms), small
+// preset 2.05 -> 1.37 ms eager and 1.27 -> 1.09 ms as a graph.
+#include <atomic>
+
 #include "common.hpp"
 
 namespace mqc {
@@ -39,6 +52,7 @@ namespace {
 typedef __bf16 skbf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 skf16x8 __attribute__((ext_vector_type(8)));
 typedef float skfloatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int sku32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSkThreads = 256;
 constexpr int kSkWaves = kSkThreads / 64;
@@ -70,6 +84,8 @@ struct SkArgs {
   int64_t n[2];
   int64_t tiles0;  // 16-row tiles of the first weight
   int64_t tiles;   // of both
+  int64_t groups0;  // 8-row groups of the first weight (wide mode)
+  int64_t groups;   // of both
   int M, K;
 };
 
@@ -170,6 +186,161 @@ __global__ __launch_bounds__(SPLIT == 1 ? kSkThreads : 64 * SPLIT) void skinny_n
   }
 }
 
+// Wide mode. A wave takes 8 weight rows at a time; lane l reads row l / 8 and
+// the 16 bytes at (l % 8) * 16 of each 128-byte line of it, so one load
+// instruction covers 8 whole lines, and all K / 64 lines of the row group are
+// issued before the first is used (LINES = K / 64 for the unrolled widths, 0
+// for any other K, which runs in groups of 8 lines). Each 16-byte piece is
+// dotted with the matching 8 k of every token, X read from LDS (the lanes of
+// one row read consecutive 16 bytes, the lanes of one piece the same ones), as
+// four dot2 instructions (two 16-bit products added to an fp32 sum). The 8
+// lanes of a row are summed by two quad permutes and a half-row mirror, after
+// which lane p holds the row's output for token p. MP: token rows padded to a
+// power of two (X rows past M are zeros in LDS and never stored).
+template <typename T> struct SkDot;
+template <> struct SkDot<bf16_t> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  __device__ static inline float dot8(v8 w, v8 x, float acc) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w, w, 0, 1), __builtin_shufflevector(x, x, 0, 1), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w, w, 2, 3), __builtin_shufflevector(x, x, 2, 3), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w, w, 4, 5), __builtin_shufflevector(x, x, 4, 5), acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w, w, 6, 7), __builtin_shufflevector(x, x, 6, 7), acc, false);
+  }
+};
+template <> struct SkDot<f16_t> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  __device__ static inline float dot8(v8 w, v8 x, float acc) {
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(w, w, 0, 1), __builtin_shufflevector(x, x, 0, 1), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(w, w, 2, 3), __builtin_shufflevector(x, x, 2, 3), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(w, w, 4, 5), __builtin_shufflevector(x, x, 4, 5), acc, false);
+    return __builtin_amdgcn_fdot2(__builtin_shufflevector(w, w, 6, 7), __builtin_shufflevector(x, x, 6, 7), acc, false);
+  }
+};
+
+constexpr int kWideThreads = 256;
+constexpr int kWideMaxRows = 8;
+constexpr int64_t kWideMinGroups = 4096;  // 8-row groups (both weights) for the wide mode
+constexpr int kWideGenericLines = 8;
+
+template <typename T, int MP, int LINES>
+__global__ __launch_bounds__(kWideThreads) void skinny_wide_kernel(SkArgs a) {
+  using D = SkDot<T>;
+  using V8 = typename D::v8;
+  constexpr int WPB = kWideThreads / 64;
+  extern __shared__ __align__(16) unsigned char sk_lds[];
+  const int K = a.K;
+  const int M = a.M;
+  {
+    // X -> LDS as MP rows of K elements, rows past M zero.
+    const int per_row = K / 8;
+    for (int i = threadIdx.x; i < MP * per_row; i += kWideThreads) {
+      sku32x4 v = {0u, 0u, 0u, 0u};
+      if (i / per_row < M) v = ((const sku32x4*)a.x)[i];
+      ((sku32x4*)sk_lds)[i] = v;
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int r = lane >> 3;  // row of the wave's group
+  const int p = lane & 7;   // 16-byte piece of each line
+  const unsigned char* xp = sk_lds + p * 16;
+  for (int64_t g = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6); g < a.groups;
+       g += (int64_t)gridDim.x * WPB) {
+    const int which = g >= a.groups0 ? 1 : 0;
+    const int64_t N = a.n[which];
+    const int64_t n = (g - (which ? a.groups0 : 0)) * 8 + r;
+    const sku32x4* wp = (const sku32x4*)((const T*)a.w[which] + (n < N ? n : N - 1) * (int64_t)K) + p;
+    float acc[MP];
+#pragma unroll
+    for (int m = 0; m < MP; ++m) acc[m] = 0.f;
+    auto consume = [&](const sku32x4& w, int line) {
+      const V8 wv = __builtin_bit_cast(V8, w);
+#pragma unroll
+      for (int m = 0; m < MP; ++m)
+        acc[m] = D::dot8(wv, *(const V8*)(xp + ((int64_t)m * K + line * 64) * 2), acc[m]);
+    };
+    // Scheduling barriers keep every load ahead of the products and the products
+    // line by line: left free, the compiler reads X for all lines before the
+    // first product and runs out of registers.
+    if constexpr (LINES > 0) {
+      sku32x4 w[LINES];
+#pragma unroll
+      for (int i = 0; i < LINES; ++i) w[i] = __builtin_nontemporal_load(wp + i * 8);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < LINES; ++i) {
+        consume(w[i], i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      const int lines = K / 64;
+      for (int c0 = 0; c0 < lines; c0 += kWideGenericLines) {
+        sku32x4 w[kWideGenericLines];
+#pragma unroll
+        for (int i = 0; i < kWideGenericLines; ++i)
+          if (c0 + i < lines) w[i] = __builtin_nontemporal_load(wp + (c0 + i) * 8);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < kWideGenericLines; ++i) {
+          if (c0 + i < lines) consume(w[i], c0 + i);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    float mine = 0.f;
+#pragma unroll
+    for (int m = 0; m < MP; ++m) {
+      float v = acc[m];
+      v += lane_xor1(v);
+      v += lane_xor2(v);
+      v += dpp_mov<0x141>(v);  // row_half_mirror: the other quad of the row's 8 lanes
+      if (p == m) mine = v;
+    }
+    if (p < M && n < N) {
+      const T* bp = (const T*)a.bias[which];
+      const float bv = bp ? io<T>::to_f32(bp[n]) : 0.f;
+      ((T*)a.y[which])[(int64_t)p * N + n] = io<T>::from_f32(mine + bv);
+    }
+  }
+}
+
+// The grid is sized to the workgroups that are resident at once, since the
+// grid-stride loop gives every workgroup an equal share: per CU, the smaller of
+// what the kernel's registers allow (looked up once per instantiation) and what
+// its LDS (X, MP x K 16-bit elements, of the CU's 160 KiB) allows.
+constexpr int64_t kCULds = 160 << 10;
+
+template <typename T, int MP, int LINES>
+int skinny_wide_launch(const SkArgs& a, hipStream_t s) {
+  static std::atomic<int> by_regs{0};
+  const size_t lds = (size_t)MP * a.K * 2;
+  int n = by_regs.load(std::memory_order_relaxed);
+  if (n == 0) {
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &n, skinny_wide_kernel<T, MP, LINES>, kWideThreads, 0);
+    if (e != hipSuccess) return (int)e;
+    if (n < 1) n = 1;
+    by_regs.store(n, std::memory_order_relaxed);
+  }
+  const int64_t by_lds = kCULds / (int64_t)lds;
+  const int64_t per_cu = by_lds < n ? (by_lds < 1 ? 1 : by_lds) : n;
+  const int64_t needed = (a.groups + kWideThreads / 64 - 1) / (kWideThreads / 64);
+  const int64_t cap = (int64_t)kSkCUs * per_cu;
+  const int64_t blocks = needed < cap ? needed : cap;
+  skinny_wide_kernel<T, MP, LINES><<<dim3((unsigned)blocks), dim3(kWideThreads), lds, s>>>(a);
+  return launch_status();
+}
+
+template <typename T, int MP>
+int skinny_wide_lines(const SkArgs& a, hipStream_t s) {
+  switch (a.K / 64) {
+    case 16: return skinny_wide_launch<T, MP, 16>(a, s);
+    case 24: return skinny_wide_launch<T, MP, 24>(a, s);
+    case 32: return skinny_wide_launch<T, MP, 32>(a, s);
+    default: return skinny_wide_launch<T, MP, 0>(a, s);
+  }
+}
+
 template <typename T, int SPLIT>
 int skinny_launch_split(const SkArgs& a, hipStream_t s) {
   constexpr int NT = SPLIT == 1 ? kSkThreads : 64 * SPLIT;
@@ -191,6 +362,16 @@ constexpr int kSkMinSteps = 4;
 
 template <typename T>
 int skinny_launch(const SkArgs& a, hipStream_t s) {
+  const int mp = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : 8;
+  if (a.M <= kWideMaxRows && a.K % 64 == 0 && a.groups >= kWideMinGroups &&
+      (int64_t)mp * a.K * 2 <= kSkMaxLds) {
+    switch (mp) {
+      case 1: return skinny_wide_lines<T, 1>(a, s);
+      case 2: return skinny_wide_lines<T, 2>(a, s);
+      case 4: return skinny_wide_lines<T, 4>(a, s);
+      default: return skinny_wide_lines<T, 8>(a, s);
+    }
+  }
   if (a.tiles >= kSkFillWaves) return skinny_launch_split<T, 1>(a, s);
   const int steps = a.K / kSkStep;
   const int64_t xlds = a.M * sk_lds_row(a.K) * 2;
@@ -238,6 +419,8 @@ extern "C" int mqc_gemm_skinny_nt(const void* X, int64_t M, int64_t K, const voi
   a.y[1] = pair ? Y2 : Y1; a.n[1] = pair ? N2 : N1;
   a.tiles0 = (N1 + 15) / 16;
   a.tiles = a.tiles0 + (pair ? (N2 + 15) / 16 : 0);
+  a.groups0 = (N1 + 7) / 8;
+  a.groups = a.groups0 + (pair ? (N2 + 7) / 8 : 0);
   a.M = (int)M;
   a.K = (int)K;
   if (dtype == MQC_BF16) return skinny_launch<bf16_t>(a, (hipStream_t)stream);

@@ -173,16 +173,31 @@ def wide_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
 # of [1024 x 1024] weights 6.3 us in one launch against about 6.6 us per weight
 # through hipBLASLt, [131072 x 1024] pairs 95-98 against 99.7 us.
 SKINNY_MAX_ROWS = 16
-# Larger weights stream faster through hipBLASLt's GEMV: the base preset's
-# [393216 x 1536] B/C pair took 420 us in one skinny launch against 409 us.
+# With at most SKINNY_WIDE_MAX_ROWS token rows and K a multiple of 64, the
+# library streams large weights in its wide mode (whole 128-byte lines per load,
+# VALU dot products), faster than hipBLASLt's GEMV: the base preset's
+# [393216 x 1536] B/C pair at 4 rows 386-392 us against 427 us (the base
+# preset's decode step 5.73 -> 5.30 ms). Other shapes keep hipBLASLt for
+# weights above SKINNY_MAX_WEIGHT_BYTES: in 16-row MFMA tiles that pair took
+# 420 us against 409 us.
+SKINNY_WIDE_MAX_ROWS = 8
 SKINNY_MAX_WEIGHT_BYTES = 512 << 20
+
+
+def _skinny_wide(rows: int, K: int) -> bool:
+    """Whether mqc_gemm_skinny_nt may stream a large weight in its wide mode:
+    at most SKINNY_WIDE_MAX_ROWS rows, K a multiple of 64, and X (rows padded
+    to a power of two) within its 64 KiB of LDS."""
+    padded = 1 << max(rows - 1, 0).bit_length()
+    return rows <= SKINNY_WIDE_MAX_ROWS and K % 64 == 0 and padded * K * 2 <= (64 << 10)
 
 
 def skinny_eligible(x: torch.Tensor, *params) -> bool:
     """Whether F.linear(x, w, b) for every (w, b) in params (flat: w1, b1, w2,
     b2, ...) may run on mqc_gemm_skinny_nt: few rows, 16-bit operands of one
-    dtype, K a multiple of 32, dense weights of at most SKINNY_MAX_WEIGHT_BYTES,
-    nothing recording autograd, no autocast, not under torch.compile."""
+    dtype, K a multiple of 32, dense weights (of at most SKINNY_MAX_WEIGHT_BYTES
+    unless the wide mode applies), nothing recording autograd, no autocast, not
+    under torch.compile."""
     if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float16) or x.dim() < 1:
         return False
     K = x.shape[-1]
@@ -194,10 +209,11 @@ def skinny_eligible(x: torch.Tensor, *params) -> bool:
     tensors = [x] + [p for p in params if p is not None]
     if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
         return False
+    wide = _skinny_wide(rows, K)
     for w, b in zip(params[0::2], params[1::2]):
         if (w.dtype != x.dtype or w.device != x.device or w.dim() != 2 or w.shape[1] != K
                 or not w.is_contiguous() or w.data_ptr() % 16
-                or w.numel() * 2 > SKINNY_MAX_WEIGHT_BYTES):
+                or (w.numel() * 2 > SKINNY_MAX_WEIGHT_BYTES and not wide)):
             return False
         if b is not None and (b.dtype != x.dtype or b.numel() != w.shape[0]
                               or not b.is_contiguous()):

@@ -18,12 +18,20 @@ DEV = "cuda"
 # Few tiles and long K take the split modes (waves sharing a tile's K):
 # (4, 768, 200) 4 waves, (4, 1536, 1000) and (4, 6144, 768) 8 (the latter held
 # there by LDS), (2, 4096, 40) 16; many tiles, or short K, one wave per tile.
+# At least 4096 groups of 8 weight rows, at most 8 token rows and K a multiple
+# of 64 take the wide mode: unrolled lines (K 1024, 1536, 2048) with 1, 2, 4
+# and 8 padded token rows, lines in groups of 8 (K 640, 4096), ragged N, the
+# 4096-group boundary; (12, 1536, 40000) has too many rows and stays in tiles.
 @pytest.mark.parametrize("M,K,N1,N2,bias", [(1, 64, 48, 0, False), (4, 1536, 1000, 0, True),
                                             (16, 96, 33, 17, True), (3, 1536, 4096, 4096, False),
                                             (7, 2016, 77, 5, True), (4, 256, 16, 16, False),
                                             (2, 32, 1, 0, True), (4, 768, 200, 0, True),
                                             (2, 4096, 40, 24, False), (4, 6144, 768, 0, True),
-                                            (4, 1024, 40000, 40000, False)])
+                                            (4, 1024, 40000, 40000, False),
+                                            (4, 1536, 40000, 40003, False), (1, 1024, 33001, 0, True),
+                                            (8, 2048, 20000, 20001, True), (5, 640, 40007, 0, True),
+                                            (3, 4096, 33000, 0, False), (2, 1536, 16384, 16384, True),
+                                            (12, 1536, 40000, 0, False)])
 def test_skinny_vs_float64(dtype, M, K, N1, N2, bias):
     g = torch.Generator(device=DEV).manual_seed(M * 1000 + K + N1)
     x = torch.randn(M, K, generator=g, device=DEV).to(dtype)
@@ -53,8 +61,14 @@ def test_skinny_eligibility():
         assert ql.skinny_eligible(x, w, None)
     with torch.autocast("cuda", dtype=torch.bfloat16):
         assert not ql.skinny_eligible(x, w.detach(), None)
+    # Weights past the bound stay off the skinny GEMM unless its wide mode
+    # applies (at most 8 rows, K a multiple of 64).
+    big = torch.empty(ql.SKINNY_MAX_WEIGHT_BYTES // 192 + 1, 96, device=DEV, dtype=torch.bfloat16)
+    assert not ql.skinny_eligible(torch.randn(4, 96, device=DEV).bfloat16(), big, None)  # K % 64
+    del big
     big = torch.empty(ql.SKINNY_MAX_WEIGHT_BYTES // 128 + 1, 64, device=DEV, dtype=torch.bfloat16)
-    assert not ql.skinny_eligible(x, big, None)
+    assert ql.skinny_eligible(x, big, None)
+    assert not ql.skinny_eligible(torch.randn(9, 64, device=DEV).bfloat16(), big, None)  # rows
 
 
 def test_skinny_entry_point_limits():
