@@ -20,9 +20,10 @@
 // blocks share lines of delta, s and y); the batch row is uniform, so the
 // start of every (b, t) slice is a wave-uniform scalar and each lane only
 // carries a 32-bit offset inside the slice. A group of G consecutive lanes
-// owns one (b, d); lane j of the group owns KPL consecutive k (one lane reads
-// KPL*4 contiguous elements of B and of C per step: 16 bytes for bf16 with
-// KPL = 2). Lanes past the last d or the last k are clamped onto valid
+// owns one (b, d); lane j of the group owns KPL states (one lane reads
+// KPL*4 elements of B and of C per step: 16 bytes for bf16 with KPL = 2,
+// contiguous; 32 bytes as two 16-byte pieces half a row apart, see SPLIT in
+// the kernel). Lanes past the last d or the last k are clamped onto valid
 // addresses instead of being branched around, so the per-step loads carry no
 // predicate; their results are discarded (past-d groups store nothing,
 // past-k lanes are zeroed before the k-sum).
@@ -89,15 +90,17 @@ __device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void* p) {
 }
 
 // Load N elements at byte offset voff (per lane) + soff (wave-uniform, added
-// by the buffer unit from an SGPR) of a buffer.
-template <typename T, int N>
+// by the buffer unit from an SGPR) of a buffer. Loads of 16 bytes or more come
+// as 16-byte pieces STRIDE bytes apart (16: contiguous); AUX is the buffer
+// instruction's cache policy (0, or 2 = NT for streams read once).
+template <typename T, int N, int AUX = 0, int STRIDE = 16>
 __device__ inline void raw_load_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, Raw<T, N>& r,
                                     uint32_t soff = 0) {
   constexpr int bytes = N * (int)sizeof(T);
   if constexpr (bytes % 16 == 0) {
 #pragma unroll
     for (int i = 0; i < bytes / 16; ++i) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 * i, soff, 0);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + STRIDE * i, soff, AUX);
       r.w[4 * i + 0] = v[0];
       r.w[4 * i + 1] = v[1];
       r.w[4 * i + 2] = v[2];
@@ -307,9 +310,35 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   const int64_t d_raw = bx * GPB + tid / G;
   const bool gvalid = d_raw < a.Dm;
   const int64_t d = gvalid ? d_raw : a.Dm - 1;
-  int k0 = j * KPL;
+  // Lane j owns KPL states. Where they take 32 bytes of B and of C per step
+  // (four 16-bit or two fp32 states) and S == KPL * G, they come as two pieces
+  // of KPL / 2 consecutive states half a (b, d) row apart, k0 + [0, KPL / 2)
+  // and k0 + S / 2 + [0, KPL / 2) with k0 = j * KPL / 2 (SPLIT): each 16-byte
+  // load instruction of a wave then reads whole 128-byte lines, which lets the
+  // loads of B and C stream with the NT cache policy. (With one contiguous
+  // 32-byte run per lane, each instruction reads half of every line it touches,
+  // and NT loads measured 11 % slower at config 3.) Otherwise the KPL states
+  // are consecutive from k0 = j * KPL.
+  constexpr bool SPLIT = FULL && KPL * 4 * (int)sizeof(T) == 32;
+  constexpr int PIECE = SPLIT ? KPL / 2 : KPL;  // consecutive states per piece
+  int k0 = j * PIECE;
   const bool kvalid = FULL || k0 < a.S;
   if (!kvalid) k0 = (int)a.S - KPL;
+  // k of the lane's state kk.
+  const int half_s = (int)a.S / 2;
+  auto kof = [&](int kk) -> int {
+    if constexpr (SPLIT) return kk >= PIECE ? k0 + half_s + (kk - PIECE) : k0 + kk;
+    return k0 + kk;
+  };
+  // Loads of B, C (and q): whole lines per instruction (16-byte lanes, or split
+  // 32-byte lanes) stream with the NT policy. Measured against the previous
+  // kernel (contiguous lanes, cached loads) on the same buffers (bf16 unless
+  // noted): config-3 inference walk 2.09-2.17 -> 1.97-2.11 ms over three
+  // allocations; training walk at config 4 2.87-2.90 -> 2.73-2.76 ms (fp16) and
+  // 2.76 -> 2.69 ms; q form B4 T1024 1.63 -> 1.56 ms; B2 S128 2.16 -> 2.10 ms.
+  constexpr int kPieceBytes = PIECE * 4 * (int)sizeof(T);
+  constexpr int LOAD_AUX = (kPieceBytes == 16) ? 2 : 0;
+  constexpr int LOAD_STRIDE = SPLIT ? 16 * G : 16;  // bytes from piece to piece: S / 2 states
 
   // Step counters are 32-bit (the host checks T): gfx9's scalar unit has no
   // 64-bit compares, and 64-bit ones would run on the VALU every step.
@@ -332,7 +361,7 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   float dskip = 0.f;
   if constexpr (MODE == MODE_DL) {
 #pragma unroll
-    for (int kk = 0; kk < KPL; ++kk) lam[kk] = lam_const(a.lam_alpha, a.lam_imag, d * a.S + k0 + kk);
+    for (int kk = 0; kk < KPL; ++kk) lam[kk] = lam_const(a.lam_alpha, a.lam_imag, d * a.S + kof(kk));
     dskip = a.dvec[d];
   }
 
@@ -344,18 +373,62 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   quat h[KPL];
 #pragma unroll
   for (int kk = 0; kk < KPL; ++kk) h[kk] = quat{0.f, 0.f, 0.f, 0.f};
+  // The lane's states in a [.., S, 4] state tensor, (b, d) row `r` (in units of
+  // S states): one run of KPL states, or the two pieces of a SPLIT lane. (The
+  // unsplit loads are written out at their two call sites: through this lambda
+  // the 1024-thread one-lane-per-(b, d) kernel needed one VGPR more than its
+  // 128 and spilled.)
+  auto load_split_states = [&](const auto* p, int64_t r) {
+    using ST = typename std::remove_cv<typename std::remove_pointer<decltype(p)>::type>::type;
+#pragma unroll
+    for (int pc = 0; pc < 2; ++pc) {
+      float e[4 * PIECE];
+      load_vec<ST, 4 * PIECE>(p + (r * a.S + kof(pc * PIECE)) * 4, e);
+#pragma unroll
+      for (int kk = 0; kk < PIECE; ++kk) h[pc * PIECE + kk] = quat_from(&e[4 * kk]);
+    }
+  };
+  auto store_states = [&](auto* p, int64_t r, auto stream) {
+    using ST = typename std::remove_pointer<decltype(p)>::type;
+    constexpr bool NTS = decltype(stream)::value;
+    float e[4 * KPL];
+#pragma unroll
+    for (int kk = 0; kk < KPL; ++kk) {
+      e[4 * kk + 0] = h[kk].w; e[4 * kk + 1] = h[kk].x;
+      e[4 * kk + 2] = h[kk].y; e[4 * kk + 3] = h[kk].z;
+    }
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int pc = 0; pc < 2; ++pc) {
+        float f[4 * PIECE];
+#pragma unroll
+        for (int i = 0; i < 4 * PIECE; ++i) f[i] = e[4 * PIECE * pc + i];
+        store_vec<ST, 4 * PIECE, NTS>(p + (r * a.S + kof(pc * PIECE)) * 4, f);
+      }
+    } else {
+      store_vec<ST, 4 * KPL, NTS>(p + (r * a.S + k0) * 4, e);
+    }
+  };
   if (chunk > 0) {
     // The state at the end of the previous chunk (fp32, from the carry prefix).
-    float e[4 * KPL];
-    load_vec<float, 4 * KPL>(
-        a.h_chunk + (((b * (a.n_chunks - 1) + chunk - 1) * a.Dm + d) * a.S + k0) * 4, e);
+    if constexpr (SPLIT) {
+      load_split_states(a.h_chunk, (b * (a.n_chunks - 1) + chunk - 1) * a.Dm + d);
+    } else {
+      float e[4 * KPL];
+      load_vec<float, 4 * KPL>(
+          a.h_chunk + (((b * (a.n_chunks - 1) + chunk - 1) * a.Dm + d) * a.S + k0) * 4, e);
 #pragma unroll
-    for (int kk = 0; kk < KPL; ++kk) h[kk] = quat_from(&e[4 * kk]);
+      for (int kk = 0; kk < KPL; ++kk) h[kk] = quat_from(&e[4 * kk]);
+    }
   } else if (a.h0) {
-    float e[4 * KPL];
-    load_vec<HT, 4 * KPL>((const HT*)a.h0 + ((b * a.Dm + d) * a.S + k0) * 4, e);
+    if constexpr (SPLIT) {
+      load_split_states((const HT*)a.h0, b * a.Dm + d);
+    } else {
+      float e[4 * KPL];
+      load_vec<HT, 4 * KPL>((const HT*)a.h0 + ((b * a.Dm + d) * a.S + k0) * 4, e);
 #pragma unroll
-    for (int kk = 0; kk < KPL; ++kk) h[kk] = quat_from(&e[4 * kk]);
+      for (int kk = 0; kk < KPL; ++kk) h[kk] = quat_from(&e[4 * kk]);
+    }
   }
 
   // Loads of step t into a ring slot. t is wave-uniform: each tensor's slice
@@ -369,10 +442,13 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
     } else {
       raw_load_buf<T, 4>(buf_rsrc((const T*)a.Sq + rt * rowTok * 4), offQ4, st.S);
       raw_load_buf<T, 1>(buf_rsrc((const T*)a.Dq + b * a.d_sb + (int64_t)t * a.d_st), offD, st.D);
-      raw_load_buf<T, 4 * KPL>(buf_rsrc((const T*)a.q + rt * rowBC), offBC, st.q);
+      raw_load_buf<T, 4 * KPL, LOAD_AUX, LOAD_STRIDE>(buf_rsrc((const T*)a.q + rt * rowBC), offBC,
+                                                      st.q);
     }
-    raw_load_buf<T, 4 * KPL>(buf_rsrc((const T*)a.Bm + rt * rowBC), offBC, st.B);
-    raw_load_buf<T, 4 * KPL>(buf_rsrc((const T*)a.Cm + rt * rowBC), offBC, st.C);
+    raw_load_buf<T, 4 * KPL, LOAD_AUX, LOAD_STRIDE>(buf_rsrc((const T*)a.Bm + rt * rowBC), offBC,
+                                                    st.B);
+    raw_load_buf<T, 4 * KPL, LOAD_AUX, LOAD_STRIDE>(buf_rsrc((const T*)a.Cm + rt * rowBC), offBC,
+                                                    st.C);
   };
 
   Step<T, MODE, KPL> ring[PF];
@@ -449,15 +525,9 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
     if (a.h_ckpt && t == next_ckpt) {
       // Chunk t / ckpt_every ends here (or the sequence does).
       if (gvalid && kvalid) {
-        float e[4 * KPL];
-#pragma unroll
-        for (int kk = 0; kk < KPL; ++kk) {
-          e[4 * kk + 0] = h[kk].w; e[4 * kk + 1] = h[kk].x;
-          e[4 * kk + 2] = h[kk].y; e[4 * kk + 3] = h[kk].z;
-        }
         // Nontemporal: the backward reads the checkpoints back after the rest of
         // the forward (the training forward measured 1-3 % faster at config 3).
-        store_vec<float, 4 * KPL, true>(a.h_ckpt + (((b * n_ckpt + ckpt_idx) * a.Dm + d) * a.S + k0) * 4, e);
+        store_states(a.h_ckpt, (b * n_ckpt + ckpt_idx) * a.Dm + d, std::true_type{});
       }
       ++ckpt_idx;
       next_ckpt = next_ckpt + ckpt_every < Tn ? next_ckpt + ckpt_every : Tn - 1;
@@ -512,15 +582,8 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
     if constexpr (SYNC == 2) __syncthreads();
   }
 
-  if (a.h_last && gvalid && kvalid && chunk == a.n_chunks - 1) {
-    float e[4 * KPL];
-#pragma unroll
-    for (int kk = 0; kk < KPL; ++kk) {
-      e[4 * kk + 0] = h[kk].w; e[4 * kk + 1] = h[kk].x;
-      e[4 * kk + 2] = h[kk].y; e[4 * kk + 3] = h[kk].z;
-    }
-    store_vec<HT, 4 * KPL>((HT*)a.h_last + ((b * a.Dm + d) * a.S + k0) * 4, e);
-  }
+  if (a.h_last && gvalid && kvalid && chunk == a.n_chunks - 1)
+    store_states((HT*)a.h_last, b * a.Dm + d, std::false_type{});
 }
 
 // Steps of operands in flight per lane (six for four 16-bit states per lane:
