@@ -32,7 +32,8 @@ namespace mqc {
 // Store one quaternion (converted from fp32) at byte offset voff + soff of a buffer,
 // nontemporal (cache policy NT): dB and dC are 2 x 6.4 GB at config 3, read back only by
 // the weight-gradient GEMMs after the whole launch; measured 5.98 -> 5.86 ms there. (The
-// same hint on the loads made the kernel 23 % slower.)
+// same hint on every load made the kernel 23 % slower; on the loads of B and C alone it
+// helps, see load_chunk.)
 template <typename T>
 __device__ inline void store_quat_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, const float (&e)[4],
                                       uint32_t soff) {
@@ -253,8 +254,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) void 
       const uint32_t ii = (uint32_t)(i < len ? i : len - 1);
       raw_load_buf<T, 1>(rD, offTok, o.rd[i], ii * stepTok);
       raw_load_buf<T, 1>(rS, offTok, o.rs[i], ii * stepTok);
-      raw_load_buf<T, 4>(rB, offBC, o.rB[i], ii * stepBC);
-      raw_load_buf<T, 4>(rC, offBC, o.rC[i], ii * stepBC);
+      // B and C with the NT cache policy: each instruction reads whole lines
+      // (64 lanes x 8 bytes, or 16 for fp32), read once (5.81-5.84 -> 5.73-5.79 ms
+      // at config 4, same buffers). On delta, s and gy, whose lines neighbouring
+      // d-blocks share, NT made the kernel 23 % slower.
+      raw_load_buf<T, 4, 2>(rB, offBC, o.rB[i], ii * stepBC);
+      raw_load_buf<T, 4, 2>(rC, offBC, o.rC[i], ii * stepBC);
       raw_load_buf<T, 4>(rG, offY, o.rg[i], ii * stepY);
     }
     // The checkpoint of the previous chunk (chunk 0 starts from h0, read in process).

@@ -91,8 +91,8 @@ __device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void* p) {
 
 // Load N elements at byte offset voff (per lane) + soff (wave-uniform, added
 // by the buffer unit from an SGPR) of a buffer. Loads of 16 bytes or more come
-// as 16-byte pieces STRIDE bytes apart (16: contiguous); AUX is the buffer
-// instruction's cache policy (0, or 2 = NT for streams read once).
+// as 16-byte pieces STRIDE bytes apart (16: contiguous); AUX is the cache
+// policy of the 16- and 8-byte loads (0, or 2 = NT for streams read once).
 template <typename T, int N, int AUX = 0, int STRIDE = 16>
 __device__ inline void raw_load_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, Raw<T, N>& r,
                                     uint32_t soff = 0) {
@@ -107,7 +107,7 @@ __device__ inline void raw_load_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, Ra
       r.w[4 * i + 3] = v[3];
     }
   } else if constexpr (bytes == 8) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, AUX);
     r.w[0] = v[0];
     r.w[1] = v[1];
   } else if constexpr (bytes == 4) {
@@ -330,14 +330,16 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
     if constexpr (SPLIT) return kk >= PIECE ? k0 + half_s + (kk - PIECE) : k0 + kk;
     return k0 + kk;
   };
-  // Loads of B, C (and q): whole lines per instruction (16-byte lanes, or split
-  // 32-byte lanes) stream with the NT policy. Measured against the previous
-  // kernel (contiguous lanes, cached loads) on the same buffers (bf16 unless
-  // noted): config-3 inference walk 2.09-2.17 -> 1.97-2.11 ms over three
+  // Loads of B, C (and q): whole lines per instruction (8- or 16-byte lanes, or
+  // split 32-byte lanes) stream with the NT policy. Measured against the
+  // previous kernel (contiguous lanes, cached loads) on the same buffers (bf16
+  // unless noted): config-3 inference walk 2.09-2.17 -> 1.97-2.11 ms over three
   // allocations; training walk at config 4 2.87-2.90 -> 2.73-2.76 ms (fp16) and
-  // 2.76 -> 2.69 ms; q form B4 T1024 1.63 -> 1.56 ms; B2 S128 2.16 -> 2.10 ms.
+  // 2.76 -> 2.69 ms; q form B4 T1024 1.63 -> 1.56 ms; B2 S128 2.16 -> 2.10 ms;
+  // one-state lanes B2 T2048 d1536 S64 1.21 -> 1.16 ms, B4 S16 0.849 -> 0.841,
+  // B1 unchanged (0.90 ms).
   constexpr int kPieceBytes = PIECE * 4 * (int)sizeof(T);
-  constexpr int LOAD_AUX = (kPieceBytes == 16) ? 2 : 0;
+  constexpr int LOAD_AUX = (kPieceBytes == 8 || kPieceBytes == 16) ? 2 : 0;
   constexpr int LOAD_STRIDE = SPLIT ? 16 * G : 16;  // bytes from piece to piece: S / 2 states
 
   // Step counters are 32-bit (the host checks T): gfx9's scalar unit has no
