@@ -91,13 +91,19 @@ __device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void* p) {
 
 // Load N elements at byte offset voff (per lane) + soff (wave-uniform, added
 // by the buffer unit from an SGPR) of a buffer. Loads of 16 bytes or more come
-// as 16-byte pieces STRIDE bytes apart (16: contiguous); AUX is the cache
-// policy of the 16- and 8-byte loads (0, or 2 = NT for streams read once).
+// as 16-byte pieces STRIDE bytes apart (16: contiguous), or a 16-byte load with
+// another STRIDE as two 8-byte pieces; AUX is the cache policy of the 16- and
+// 8-byte loads (0, or 2 = NT for streams read once).
 template <typename T, int N, int AUX = 0, int STRIDE = 16>
 __device__ inline void raw_load_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, Raw<T, N>& r,
                                     uint32_t soff = 0) {
   constexpr int bytes = N * (int)sizeof(T);
-  if constexpr (bytes % 16 == 0) {
+  if constexpr (STRIDE != 16 && bytes == 16) {
+    // Two 8-byte pieces STRIDE bytes apart.
+    const auto v0 = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, AUX);
+    const auto v1 = __builtin_amdgcn_raw_buffer_load_b64(rs, voff + STRIDE, soff, AUX);
+    r.w[0] = v0[0]; r.w[1] = v0[1]; r.w[2] = v1[0]; r.w[3] = v1[1];
+  } else if constexpr (bytes % 16 == 0) {
 #pragma unroll
     for (int i = 0; i < bytes / 16; ++i) {
       const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + STRIDE * i, soff, AUX);
@@ -311,15 +317,21 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   const bool gvalid = d_raw < a.Dm;
   const int64_t d = gvalid ? d_raw : a.Dm - 1;
   // Lane j owns KPL states. Where they take 32 bytes of B and of C per step
-  // (four 16-bit or two fp32 states) and S == KPL * G, they come as two pieces
-  // of KPL / 2 consecutive states half a (b, d) row apart, k0 + [0, KPL / 2)
-  // and k0 + S / 2 + [0, KPL / 2) with k0 = j * KPL / 2 (SPLIT): each 16-byte
-  // load instruction of a wave then reads whole 128-byte lines, which lets the
-  // loads of B and C stream with the NT cache policy. (With one contiguous
-  // 32-byte run per lane, each instruction reads half of every line it touches,
-  // and NT loads measured 11 % slower at config 3.) Otherwise the KPL states
-  // are consecutive from k0 = j * KPL.
-  constexpr bool SPLIT = FULL && KPL * 4 * (int)sizeof(T) == 32;
+  // (four 16-bit or two fp32 states), or are two 16-bit states, and S == KPL * G,
+  // they come as two pieces of KPL / 2 consecutive states half a (b, d) row
+  // apart, k0 + [0, KPL / 2) and k0 + S / 2 + [0, KPL / 2) with k0 = j * KPL / 2
+  // (SPLIT): each load instruction of a wave then reads whole 128-byte lines,
+  // which lets the loads of B and C stream with the NT cache policy. (With one
+  // contiguous 32-byte run per lane, each instruction reads half of every line
+  // it touches, and NT loads measured 11 % slower at config 3.) For two 16-bit
+  // states the pieces are 8 bytes of B and C, and one state (16 bytes of fp32)
+  // of the training walk's checkpoints, so each checkpoint store instruction
+  // writes whole lines too: training walk at config 4 2.70-2.75 -> 2.58-2.63 ms
+  // (fp16), 2.78-2.79 -> 2.63-2.64 ms (bf16), same buffers, against contiguous
+  // two-state lanes with NT loads. Otherwise the KPL states are consecutive
+  // from k0 = j * KPL.
+  constexpr bool SPLIT =
+      FULL && (KPL * 4 * (int)sizeof(T) == 32 || (KPL == 2 && sizeof(T) == 2));
   constexpr int PIECE = SPLIT ? KPL / 2 : KPL;  // consecutive states per piece
   int k0 = j * PIECE;
   const bool kvalid = FULL || k0 < a.S;
@@ -340,7 +352,8 @@ __global__ __launch_bounds__(NT) void ssm_scan_kernel(SsmArgs a) {
   // B1 unchanged (0.90 ms).
   constexpr int kPieceBytes = PIECE * 4 * (int)sizeof(T);
   constexpr int LOAD_AUX = (kPieceBytes == 8 || kPieceBytes == 16) ? 2 : 0;
-  constexpr int LOAD_STRIDE = SPLIT ? 16 * G : 16;  // bytes from piece to piece: S / 2 states
+  // Bytes from piece to piece: S / 2 states.
+  constexpr int LOAD_STRIDE = SPLIT ? (KPL / 2) * 4 * (int)sizeof(T) * G : 16;
 
   // Step counters are 32-bit (the host checks T): gfx9's scalar unit has no
   // 64-bit compares, and 64-bit ones would run on the VALU every step.
