@@ -43,6 +43,9 @@ extern "C" {
                               * stated maximum, one (b, t) slice of B/C of 2 GiB or
                               * more, or a negative or too large D stride) */
 #define MQC_E_SPACE (-6)     /* a workspace is smaller than the call needs */
+#define MQC_E_OVERLAP (-7)   /* an output overlaps an input that the launch still reads
+                              * (the chunked SSM walks: h_last over h0, dh0 over
+                              * dh_last) */
 
 /* Human-readable text for a status code (static storage, never NULL). */
 const char* mqc_status_string(int status);
@@ -126,7 +129,8 @@ int mqc_ssm_fused_fwd(const void* delta, const void* s, const void* B, const voi
  * the library choose: seq_len (one chunk, the whole walk) when batch * d_inner
  * * d_state states keep the GPU busy on their own, shorter chunks when they
  * do not: about 393216 / states chunks, each at least 64 steps, at most 1024
- * chunks. Negative: an MQC_E_* code. */
+ * chunks and at most 65535 / batch (the chunked launches' limit on
+ * batch * n_chunks). Negative: an MQC_E_* code. */
 int64_t mqc_ssm_chunk_len_auto(int64_t batch, int64_t seq_len, int64_t d_inner,
                                int64_t d_state, int dtype);
 
@@ -147,6 +151,8 @@ int64_t mqc_ssm_chunked_workspace_bytes(int64_t batch, int64_t seq_len, int64_t 
  * mqc_ssm_chunked_workspace_bytes (16-byte aligned; may be NULL when
  * chunk_len >= seq_len), owned by the caller, no contents needed on entry.
  * d_state <= 64 when there is more than one chunk; batch * n_chunks <= 65535.
+ * Unlike the whole walk, with more than one chunk h_last may not overlap h0
+ * (MQC_E_OVERLAP): chunk 0 reads h0 while the last chunk writes h_last.
  * Replaces, like mqc_ssm_fused_fwd, mambaqc/models/quaternion_mamba2_block.py:206-228
  * (the sequential walk of kernels/ssm_fused.py:363-379); the chunked order of
  * evaluation follows the associative-scan idea of kernels/parallel_scan.py:171-264. */
@@ -178,6 +184,15 @@ int mqc_ssm_fused_fwd_chunked_noalloc(const void* delta, const void* s, const vo
 
 /* Size in bytes of the fixed device scratch of mqc_ssm_fused_fwd_chunked_noalloc. */
 int64_t mqc_ssm_chunked_scratch_bytes(void);
+
+/* Looks up the current device's address of that scratch, which
+ * mqc_ssm_fused_fwd_chunked_noalloc otherwise looks up (hipGetSymbolAddress)
+ * on its first call on each device. Call it once per device, with the device
+ * current, before capturing no-alloc calls into a HIP graph, so that the
+ * captured calls make no HIP runtime call but their kernel launches.
+ * Idempotent and thread-safe. Returns MQC_OK or a hipError_t. No counterpart
+ * in the reference. */
+int mqc_ssm_noalloc_prepare(void);
 
 /* C[M, N] = X[M, K] . W[N, K]^T in bf16 with fp32 accumulation (dtype must be
  * MQC_BF16), contiguous row-major X, W, C, 16-byte aligned; N a multiple of
@@ -305,7 +320,8 @@ int mqc_ssm_fused_bwd(const void* delta, const void* s, const void* B, const voi
  * (the checkpoints are the whole walk's, at the same steps); workspace holds
  * mqc_ssm_chunked_workspace_bytes(batch, seq_len, d_inner, d_state, chunk_len)
  * bytes (16-byte aligned; MQC_E_SPACE if smaller); d_state <= 64. chunk_len >=
- * seq_len is the whole walk (no workspace used). No counterpart in the
+ * seq_len is the whole walk (no workspace used). With more than one chunk
+ * h_last may not overlap h0 (MQC_E_OVERLAP). No counterpart in the
  * reference (its GPU path has no training forward). */
 int mqc_ssm_fused_fwd_train_chunked(const void* delta, const void* s, const void* B,
                                     const void* C, const float* lambda_alpha,
@@ -321,7 +337,8 @@ int mqc_ssm_fused_fwd_train_chunked(const void* delta, const void* s, const void
  * mqc_ssm_fused_fwd_train_chunked). With n_chunks = ceil(seq_len / chunk_len)
  * > 1 the parameter partials have n_chunks * batch rows
  * (dlambda_alpha_part fp32 [n_chunks * batch, d_inner, d_state], and so on; the
- * caller sums the first axis); chunk_len >= seq_len is mqc_ssm_fused_bwd. No
+ * caller sums the first axis); chunk_len >= seq_len is mqc_ssm_fused_bwd.
+ * With more than one chunk dh0 may not overlap dh_last (MQC_E_OVERLAP). No
  * counterpart in the reference. */
 int mqc_ssm_fused_bwd_chunked(const void* delta, const void* s, const void* B, const void* C,
                               const float* lambda_alpha, const float* lambda_imag, const float* D,

@@ -68,6 +68,7 @@ SIGNATURES = {
                                   _i64, _i64, _f32, _int, _vp, _i64, _vp],
     "mqc_ssm_fused_fwd_chunked_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                           _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp],
+    "mqc_ssm_noalloc_prepare": [],
 }
 
 # name -> argtypes of the entry points that return int64_t (a size, or a
@@ -78,7 +79,7 @@ SIGNATURES_I64 = {
     "mqc_ssm_chunked_scratch_bytes": [],
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib = None

@@ -262,4 +262,12 @@ inline int launch_status() {
 
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// Whether the byte ranges [a, a + na) and [b, b + nb) share a byte (NULL or
+// empty ranges share none).
+inline bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
+  if (!a || !b || na <= 0 || nb <= 0) return false;
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + (uintptr_t)nb && y < x + (uintptr_t)na;
+}
+
 }  // namespace mqc

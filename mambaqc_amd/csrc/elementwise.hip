@@ -427,11 +427,12 @@ const char* mqc_status_string(int status) {
     case MQC_E_ALIGN: return "a pointer is not aligned for the kernel's vector loads";
     case MQC_E_LIMIT: return "a size is beyond what the kernels support";
     case MQC_E_SPACE: return "the workspace (or the library's fixed scratch) is smaller than the call needs";
+    case MQC_E_OVERLAP: return "an output overlaps an input the launch still reads (chunked walks take no in-place state)";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
   }
 }
 
-int mqc_abi_version(void) { return 5; }
+int mqc_abi_version(void) { return 6; }
 
 int mqc_quaternion_multiply(const void* p, const void* q, void* out, int64_t n_quat, int dtype,
                             void* stream) {

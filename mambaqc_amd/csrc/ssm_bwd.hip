@@ -125,6 +125,10 @@ int mqc_ssm_fused_fwd_train_chunked(const void* delta, const void* s, const void
     return MQC_E_NULL;
   if (d_inner > (1LL << 24)) return MQC_E_LIMIT;
   if (!aligned(h_ckpt, 16)) return MQC_E_ALIGN;
+  // As in mqc_ssm_fused_fwd_chunked: chunk 0 reads h0, the last chunk writes
+  // h_last, in one launch.
+  const int64_t state_bytes = batch * d_inner * d_state * 4 * (int64_t)sizeof(float);
+  if (overlaps(h0, state_bytes, h_last, state_bytes)) return MQC_E_OVERLAP;
   SsmArgs a{};
   a.delta = delta; a.s = s; a.lam_alpha = lambda_alpha; a.lam_imag = lambda_imag; a.dvec = D;
   a.Bm = B; a.Cm = C; a.h0 = h0; a.y = y; a.h_last = h_last;
@@ -165,6 +169,10 @@ int mqc_ssm_fused_bwd_chunked(const void* delta, const void* s, const void* B, c
     return MQC_E_NULL;
   if (d_inner > (1LL << 24) || d_state > 64) return MQC_E_LIMIT;
   if (ckpt_every != mqc_ssm_bwd_ckpt_every(dtype)) return MQC_E_LIMIT;
+  // The last chunk reads dh_last as it starts and chunk 0 writes dh0 as it
+  // ends, in one launch.
+  const int64_t state_bytes = batch * d_inner * d_state * 4 * (int64_t)sizeof(float);
+  if (overlaps(dh_last, state_bytes, dh0, state_bytes)) return MQC_E_OVERLAP;
   SsmBwdArgs a{};
   a.delta = delta; a.s = s; a.Bm = B; a.Cm = C; a.lam_alpha = lambda_alpha;
   a.lam_imag = lambda_imag; a.dvec = D; a.h0 = (const float*)h0; a.h_ckpt = h_ckpt; a.gy = gy;

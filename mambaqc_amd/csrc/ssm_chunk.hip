@@ -64,7 +64,10 @@ int64_t auto_chunk_len(int64_t batch, int64_t T, int64_t Dm, int64_t S) {
   int64_t nc = (kBusyStates + states - 1) / states;
   if (nc > kMaxChunks) nc = kMaxChunks;
   if (nc > T / kMinChunk) nc = T / kMinChunk;
+  // The chunked launches put batch * n_chunks blocks on the grid's y axis.
+  if (nc > 65535 / batch) nc = 65535 / batch;
   if (nc <= 1) return T;
+  // ceil(T / L) never exceeds nc for L = ceil(T / nc).
   return (T + nc - 1) / nc;
 }
 
@@ -72,8 +75,9 @@ int64_t auto_chunk_len(int64_t batch, int64_t T, int64_t Dm, int64_t S) {
 // with *nothing set when there is nothing to launch.
 int check_chunked(const void* delta, const void* s, const void* B, const void* C,
                   const float* lambda_alpha, const float* lambda_imag, const float* D,
-                  const void* y, const void* h_last, int64_t batch, int64_t seq_len,
-                  int64_t d_inner, int64_t d_state, int64_t chunk_len, int dtype, bool& nothing) {
+                  const void* h0, const void* y, const void* h_last, int64_t batch,
+                  int64_t seq_len, int64_t d_inner, int64_t d_state, int64_t chunk_len,
+                  int dtype, bool& nothing) {
   nothing = false;
   if (batch < 0 || seq_len < 0 || d_inner < 0 || d_state < 0 || chunk_len < 1) return MQC_E_SHAPE;
   if (dtype != MQC_F32 && dtype != MQC_BF16 && dtype != MQC_F16) return MQC_E_DTYPE;
@@ -84,6 +88,12 @@ int check_chunked(const void* delta, const void* s, const void* B, const void* C
   if ((steps || state_only) && (!lambda_alpha || !lambda_imag || !D)) return MQC_E_NULL;
   if (batch > 65535 || d_inner > (1LL << 24) || d_state > 256) return MQC_E_LIMIT;
   nothing = !steps && !state_only;
+  // With more than one chunk, chunk 0 reads h0 as it starts and the last chunk
+  // writes h_last as it ends, in blocks of one launch that run in no fixed
+  // order: no in-place state (the whole walk allows it).
+  const int64_t state_bytes = batch * d_inner * d_state * 4 * (int64_t)sizeof(float);
+  if (steps && seq_len > chunk_len && overlaps(h0, state_bytes, h_last, state_bytes))
+    return MQC_E_OVERLAP;
   return MQC_OK;
 }
 
@@ -116,8 +126,8 @@ int mqc_ssm_fused_fwd_chunked(const void* delta, const void* s, const void* B, c
                               int64_t chunk_len, float eps, int dtype, void* workspace,
                               int64_t workspace_bytes, void* stream) {
   bool nothing;
-  int st = check_chunked(delta, s, B, C, lambda_alpha, lambda_imag, D, y, h_last, batch, seq_len,
-                         d_inner, d_state, chunk_len, dtype, nothing);
+  int st = check_chunked(delta, s, B, C, lambda_alpha, lambda_imag, D, h0, y, h_last, batch,
+                         seq_len, d_inner, d_state, chunk_len, dtype, nothing);
   if (st != MQC_OK || nothing) return st;
   SsmArgs a{};
   a.delta = delta; a.s = s; a.lam_alpha = lambda_alpha; a.lam_imag = lambda_imag; a.dvec = D;
@@ -149,6 +159,11 @@ int mqc_ssm_fused_fwd_chunked(const void* delta, const void* s, const void* B, c
 
 int64_t mqc_ssm_chunked_scratch_bytes(void) { return kScratchBytes; }
 
+int mqc_ssm_noalloc_prepare(void) {
+  void* p = nullptr;
+  return scratch_ptr(&p);
+}
+
 int mqc_ssm_fused_fwd_chunked_noalloc(const void* delta, const void* s, const void* B,
                                       const void* C, const float* lambda_alpha,
                                       const float* lambda_imag, const float* D, const void* h0,
@@ -156,8 +171,8 @@ int mqc_ssm_fused_fwd_chunked_noalloc(const void* delta, const void* s, const vo
                                       int64_t d_inner, int64_t d_state, int64_t chunk_len,
                                       float eps, int dtype, void* stream) {
   bool nothing;
-  int st = check_chunked(delta, s, B, C, lambda_alpha, lambda_imag, D, y, h_last, batch, seq_len,
-                         d_inner, d_state, chunk_len, dtype, nothing);
+  int st = check_chunked(delta, s, B, C, lambda_alpha, lambda_imag, D, h0, y, h_last, batch,
+                         seq_len, d_inner, d_state, chunk_len, dtype, nothing);
   if (st != MQC_OK || nothing) return st;
   const int64_t nc = seq_len > chunk_len ? (seq_len + chunk_len - 1) / chunk_len : 1;
   if (nc > 1 && d_state > kChunkMaxState) return MQC_E_LIMIT;

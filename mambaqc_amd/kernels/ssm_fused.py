@@ -144,9 +144,14 @@ def train_chunk_len(batch: int, seq_len: int, d_inner: int, d_state: int,
     K = int(nat.load().mqc_ssm_bwd_ckpt_every(code))
     if chunk_len is not None and int(chunk_len) < 1:
         raise ValueError(f"chunk_len must be >= 1, got {chunk_len}")
-    L = chunk_len_for(batch, seq_len, d_inner, d_state, dtype) if chunk_len is None \
-        else int(chunk_len)
-    return -(-L // K) * K
+    if chunk_len is not None:
+        return -(-int(chunk_len) // K) * K
+    L = -(-chunk_len_for(batch, seq_len, d_inner, d_state, dtype) // K) * K
+    # Rounding up only lowers the chunk count, so the library's bound on
+    # batch * n_chunks (65535) still holds; kept explicit for the launches.
+    if L < seq_len and batch * -(-seq_len // L) > 65535:
+        return seq_len
+    return L
 
 
 def _chunk_workspace(batch, T, d_inner, d_state, L, device):
@@ -456,8 +461,13 @@ def ssm_forward_front_dl(dt_raw: torch.Tensor, g_raw: torch.Tensor, x: torch.Ten
     inputs = (dt_raw, g_raw, x, B, C, lambda_alpha, lambda_imag, D) + (
         (h0,) if h0 is not None else ())
     if nat.compiling():
-        # Front and SSM as two traced operators (the eager path keeps them in
-        # one autograd node so that d_delta reaches the front in fp32).
+        if torch.is_grad_enabled() and any(t.requires_grad for t in inputs):
+            # Front and training walk as one traced operator, whose backward
+            # hands d_delta and d_s to the front in fp32 (as _SsmFrontFusedDL).
+            _require_trainable_state(B)
+            y, h_last, _ = torch.ops.mambaqc.ssm_front_forward_dl_train(
+                dt_raw, g_raw, x, B, C, lambda_alpha, lambda_imag, D, h0, eps)
+            return (y, h_last) if return_state else y
         delta, s = torch.ops.mambaqc.ssm_front(dt_raw, g_raw, x)
         return _dl_ops(delta, s, B, C, lambda_alpha, lambda_imag, D, h0, eps, return_state,
                        None, inputs)

@@ -273,6 +273,55 @@ def _front_bwd(ctx, g_delta, g_s):
 register_autograd(f"{NS}::ssm_front", _front_bwd, setup_context=_front_setup)
 
 
+# --- front + training walk as one operator ------------------------------------
+# Under torch.compile with autograd, the front and the SSM's training walk are
+# one operator so that the SSM's fp32 d_delta and d_s reach the front's
+# backward without passing through delta's dtype (fp16/bf16 under autocast),
+# as the eager _SsmFrontFusedDL does.
+
+@custom_op(f"{NS}::ssm_front_forward_dl_train", mutates_args=())
+def ssm_front_forward_dl_train(dt_raw: Tensor, g_raw: Tensor, x: Tensor, B: Tensor, C: Tensor,
+                               lambda_alpha: Tensor, lambda_imag: Tensor, D: Tensor,
+                               h0: Optional[Tensor] = None,
+                               eps: float = 1e-6) -> Tuple[Tensor, Tensor, Tensor]:
+    """(y, h_last fp32, fp32 checkpoints) of the training walk from the
+    projections' outputs: delta = softplus(dt_raw), s = sigmoid(g_raw) * x."""
+    dt, g, xv = sf._front_operands(dt_raw, g_raw, x)
+    delta, s = sf._front_forward(dt, g, xv)
+    y, h_last, saved = sf.ssm_fused_dl_train_forward(delta, s, B, C, lambda_alpha,
+                                                     lambda_imag, D, h0, eps)
+    return y, h_last, saved[-1]
+
+
+@ssm_front_forward_dl_train.register_fake
+def _(dt_raw, g_raw, x, B, C, lambda_alpha, lambda_imag, D, h0=None, eps=1e-6):
+    b, t, d, n, _ = B.shape
+    return (B.new_empty(b, t, d, 4), B.new_empty(b, d, n, 4, dtype=torch.float32),
+            B.new_empty(*_ckpt_shape(B), dtype=torch.float32))
+
+
+def _front_train_setup(ctx, inputs, output):
+    dt_raw, g_raw, x, B, C, la, li, D, h0, eps = inputs
+    ctx.save_for_backward(dt_raw, g_raw, x, B, C, la, li, D, h0, output[2])
+    ctx.eps = eps
+
+
+def _front_train_backward(ctx, gy, gh_last, _gckpt):
+    dt_raw, g_raw, x, B, C, la, li, D, h0, ckpt = ctx.saved_tensors
+    delta, s = ssm_front(dt_raw, g_raw, x)
+    d_delta, d_s, dB, dC, dla, dli, dD, dh0 = ssm_backward_dl(
+        delta, s, B, C, la, li, D, h0, ckpt, gy, gh_last, ctx.eps)
+    # d_delta and d_s stay fp32 into the front's backward.
+    d_dt, d_g, d_x = ssm_front_backward(dt_raw, g_raw, x, d_delta, d_s)
+    return (d_dt.to(dt_raw.dtype), d_g.to(g_raw.dtype), d_x.to(x.dtype), dB, dC,
+            dla.to(la.dtype), dli.to(li.dtype), dD.to(D.dtype),
+            None if h0 is None else dh0.to(h0.dtype), None)
+
+
+register_autograd(f"{NS}::ssm_front_forward_dl_train", _front_train_backward,
+                  setup_context=_front_train_setup)
+
+
 # --- Quaternion LayerNorm (quaternion_norm.py:119-245) ------------------------
 
 @custom_op(f"{NS}::quaternion_layer_norm", mutates_args=())

@@ -299,6 +299,52 @@ def test_block_forward_backward_config4_fp16_autocast():
         assert rel < 5e-2, f"config 4 d{n}: fp16-autocast vs fp32 relative error {rel:.3g}"
 
 
+def _close_on_device(got, ref, rtol, what):
+    """assert_close's bound (rtol * |ref| + rtol * max|ref|) evaluated on the
+    GPU in fp32, for gradients too large to copy to the host as float64."""
+    got = got.float()
+    ref = ref.float()
+    assert got.shape == ref.shape, what
+    assert torch.isfinite(got).all(), f"{what}: non-finite values"
+    scale = ref.abs().max()
+    excess = (got - ref).abs() - rtol * (ref.abs() + scale)
+    worst = int(torch.argmax(excess))
+    assert excess.reshape(-1)[worst] <= 0, (
+        f"{what}: {int((excess > 0).sum())}/{ref.numel()} out of rtol {rtol}; worst at "
+        f"{worst}: got {got.reshape(-1)[worst].item():.6g}, ref {ref.reshape(-1)[worst].item():.6g}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_wide_linear_backward_at_projection_shape(dtype):
+    """The B/C projections' blocked GEMMs at the shape config 4 trains them:
+    K 1536 inputs, N 393 216 outputs (d_inner 1536 x d_state 64 x 4), here
+    1024 token rows (the blocked path's threshold). The forward by column
+    blocks, dX as one batched GEMM over equal K blocks with fp32 partials, dW
+    by row blocks, against one unblocked F.linear with autograd in fp32 on the
+    same rounded operands (torch's GEMM as the third-party reference)."""
+    from mambaqc_amd.layers import quaternion_linear as ql
+
+    m, k, n = 1024, 1536, 393216
+    print(f"wide_linear backward {dtype} M{m} K{k} N{n}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(21)
+    x = torch.randn(m, k, generator=g, device=DEV).to(dtype)
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(dtype)
+    gy = torch.randn(m, n, generator=g, device=DEV).to(dtype)
+    es = w.element_size()
+    assert len(ql._blocks(n, k, es)) > 1 and ql._dx_batches(n, k, es) >= 8
+    assert m >= ql.WIDE_LINEAR_MIN_ROWS
+    xb, wb = _leaf(x), _leaf(w)
+    y = ql.wide_linear(xb, wb)
+    assert isinstance(y.grad_fn, torch.autograd.function.BackwardCFunction)
+    y.backward(gy)
+    xf, wf = _leaf(x.float()), _leaf(w.float())
+    yf = torch.nn.functional.linear(xf, wf)
+    yf.backward(gy.float())
+    _close_on_device(y, yf, 2e-2, f"wide_linear y {dtype}")
+    _close_on_device(xb.grad, xf.grad, 2e-2, f"wide_linear dX {dtype}")
+    _close_on_device(wb.grad, wf.grad, 2e-2, f"wide_linear dW {dtype}")
+
+
 @pytest.mark.parametrize("shape", [(2, 37, 48, 4), (1, 3, 16, 4), (2, 20, 13, 3), (3, 33, 64, 6)])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_causal_conv_silu_backward(shape, dtype):

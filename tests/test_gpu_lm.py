@@ -120,6 +120,29 @@ def test_lm_backward_vs_oracle():
         assert_close(p.grad, sd[name].grad, 1e-4, f"LM d{name}")
 
 
+def test_lm_base_width_vs_oracle():
+    """Two layers of the base preset's width (d_model 768, d_state 64, expand 2,
+    vocab 10000) in bf16 at B1 T64 against the CPU oracle in fp32 on the same
+    bf16-rounded weights: the blocks at config 5's shape (the 4-state SSM
+    lanes, the B/C projections' column blocks) compared with a reference, not
+    with themselves."""
+    torch.manual_seed(0)
+    with torch.device(DEV):
+        lm = mambaqc_amd.QuaternionMamba2(10000, d_model=768, n_layers=2, d_state=64,
+                                          d_conv=4, expand_factor=2)
+    lm = lm.to(torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(3)
+    ids = torch.randint(0, 10000, (1, 64), generator=g)
+    print("LM base width, 2 layers, B1 T64, bf16", flush=True)
+    with torch.inference_mode():
+        got = lm(ids.to(DEV))["logits"]
+    sd = {k: v.detach().float().cpu() for k, v in lm.state_dict().items()}
+    del lm
+    want, _ = oracle.lm_forward_reference(sd, ids, n_layers=2, d_state=64, vocab_size=10000)
+    assert got.shape == want.shape == (1, 64, 10000)
+    assert_close(got, want, 2e-2, "LM logits, base width (bf16 vs fp32 oracle)")
+
+
 def test_lm_base_config5_forward():
     """Config 5: the base preset (12 layers, d_model 768, d_state 64; 14.66 B
     parameters) in bf16, B4 T2048, vocab 10000. Logits are finite, and causal:

@@ -97,6 +97,9 @@ def test_opcheck():
     opcheck(mm.cumprod_scan, (z,))
     delta, s, B, C, la, li, D, h0 = _dl_inputs(dtype=torch.float32, t=13, grad=True)
     opcheck(mm.ssm_forward_dl_train, (delta, s, B, C, la, li, D, h0, 1e-6))
+    dtr = torch.randn(delta.shape, generator=g, device=DEV, requires_grad=True)
+    grr = torch.randn(delta.shape, generator=g, device=DEV, requires_grad=True)
+    opcheck(mm.ssm_front_forward_dl_train, (dtr, grr, s, B, C, la, li, D, h0, 1e-6))
     with torch.no_grad():
         opcheck(mm.ssm_forward_dl, (delta, s, B, C, la, li, D, None, 1e-6, None))
     x = torch.randn(2, 7, 6, generator=g, device=DEV, requires_grad=True)
@@ -126,6 +129,29 @@ def test_ssm_train_op_gradients_equal_autograd_function(dtype):
     got = _grads((y, hl), ins)
     ins2 = [t.detach().requires_grad_() for t in ins]
     y2, hl2 = K.ssm_forward_fused_dl(*ins2[:7], eps=1e-6, h0=ins2[7], return_state=True)
+    want = _grads((y2, hl2), ins2)
+    assert torch.equal(y, y2) and torch.equal(hl, hl2)
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert torch.equal(a, b), f"grad {i}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_front_train_op_gradients_equal_autograd_function(dtype):
+    """The front + training-walk operator (what torch.compile traces while
+    autograd records) against the eager _SsmFrontFusedDL: the same kernels in
+    the same order, d_delta and d_s fp32 into the front's backward in both, so
+    equal bit for bit (fp16 included, where a round trip through delta's dtype
+    would not be)."""
+    _, _, B, C, la, li, D, h0 = _dl_inputs(dtype=dtype, seed=3)
+    g = _g(4)
+    dt = torch.randn(B.shape[:3], generator=g, device=DEV).to(dtype)
+    gr = torch.randn(B.shape[:3], generator=g, device=DEV).to(dtype)
+    x = torch.randn(B.shape[:3], generator=g, device=DEV).to(dtype)
+    ins = [t.detach().requires_grad_() for t in (dt, gr, x, B, C, la, li, D, h0)]
+    y, hl, _ = mm.ssm_front_forward_dl_train(*ins, 1e-6)
+    got = _grads((y, hl), ins)
+    ins2 = [t.detach().requires_grad_() for t in ins]
+    y2, hl2 = K.ssm_forward_front_dl(*ins2[:8], eps=1e-6, h0=ins2[8], return_state=True)
     want = _grads((y2, hl2), ins2)
     assert torch.equal(y, y2) and torch.equal(hl, hl2)
     for i, (a, b) in enumerate(zip(got, want)):
@@ -222,3 +248,27 @@ def test_block_compiles_fullgraph(dtype, rtol):
     names = ["x"] + [n for n, _ in blk.named_parameters()]
     for n, a, b in zip(names, gc, ge):
         assert_close(a, b, max(rtol, 1e-4), f"compiled block grad {n}")
+
+
+def test_block_compiles_fullgraph_fp16_autocast():
+    """The compiled block under fp16 autocast (config 4's precision): forward
+    and gradients against the eager block. The traced front + SSM is one
+    operator, so d_delta and d_s reach the front's backward in fp32 as in the
+    eager path."""
+    torch.manual_seed(5)
+    blk = mambaqc_amd.QuaternionMamba2Block(32, d_state=8).to(DEV)
+    x = torch.randn(2, 40, 32, generator=_g(6), device=DEV)
+    compiled = torch.compile(blk, backend="aot_eager", fullgraph=True)
+    gy = torch.randn(2, 40, 32, generator=_g(7), device=DEV)
+    xe = x.clone().requires_grad_()
+    xc = x.clone().requires_grad_()
+    from conftest import assert_close
+    with torch.autocast("cuda", dtype=torch.float16):
+        ye = blk(xe)
+        yc = compiled(xc)
+    ge = torch.autograd.grad(ye.float(), [xe] + list(blk.parameters()), gy)
+    gc = torch.autograd.grad(yc.float(), [xc] + list(blk.parameters()), gy)
+    assert_close(yc, ye, 2e-2, "compiled block forward (fp16 autocast)")
+    names = ["x"] + [n for n, _ in blk.named_parameters()]
+    for n, a, b in zip(names, gc, ge):
+        assert_close(a, b, 2e-2, f"compiled block grad {n} (fp16 autocast)")

@@ -29,7 +29,7 @@ def declared_symbols():
 
 def test_header_declares_the_api():
     names = declared_symbols()
-    assert len(names) == 32, names
+    assert len(names) == 33, names
     assert set(nat.SIGNATURES) | set(nat.SIGNATURES_I64) <= set(names)
 
 
@@ -37,12 +37,12 @@ def test_library_exports_every_declared_symbol():
     lib = nat.load()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mqc_abi_version() == nat.ABI_VERSION == 5
+    assert lib.mqc_abi_version() == nat.ABI_VERSION == 6
 
 
 def test_status_strings():
     assert nat.status_string(0) == "ok"
-    for code in (-1, -2, -3, -4, -5, -6):
+    for code in (-1, -2, -3, -4, -5, -6, -7):
         s = nat.status_string(code)
         assert s and s != "unknown status"
 
@@ -197,6 +197,51 @@ def test_chunk_policy_and_workspace_without_gpu():
                                          FAKE, need - 1, None) == -6
     assert lib.mqc_ssm_fused_fwd_chunked(*P, None, FAKE, None, 1, 100, 4, 65, 10, 1e-6, 1,
                                          FAKE, 1 << 40, None) == -5
+
+
+def test_chunked_walks_refuse_in_place_state_without_gpu():
+    """With more than one chunk, chunk 0 reads h0 while the last chunk writes
+    h_last in the same launch: the chunked entry points refuse overlapping
+    state buffers (MQC_E_OVERLAP) before any HIP call; the whole walk (one
+    chunk) keeps taking h_last == h0."""
+    lib = nat.load()
+    P = [FAKE] * 7
+    b, T, d, k, L = 1, 100, 4, 8, 10
+    nbytes = b * d * k * 16
+    need = lib.mqc_ssm_chunked_workspace_bytes(b, T, d, k, L)
+    H = ctypes.c_void_p(1 << 20)
+    H_part = ctypes.c_void_p((1 << 20) + nbytes - 16)
+    H_next = ctypes.c_void_p((1 << 20) + nbytes)
+    for h_last in (H, H_part):
+        assert lib.mqc_ssm_fused_fwd_chunked(*P, H, FAKE, h_last, b, T, d, k, L, 1e-6, 1,
+                                             FAKE, need, None) == -7
+        assert lib.mqc_ssm_fused_fwd_chunked_noalloc(*P, H, FAKE, h_last, b, T, d, k, L,
+                                                     1e-6, 1, None) == -7
+    # Adjacent buffers pass this check and fail the next one (no workspace).
+    assert lib.mqc_ssm_fused_fwd_chunked(*P, H, FAKE, H_next, b, T, d, k, L, 1e-6, 1,
+                                         None, need, None) == -1
+    K = lib.mqc_ssm_bwd_ckpt_every(1)
+    Lk = K * 2
+    need_k = lib.mqc_ssm_chunked_workspace_bytes(b, T, d, k, Lk)
+    assert lib.mqc_ssm_fused_fwd_train_chunked(*P, H, FAKE, H, FAKE, K, b, T, d, k, Lk, 1e-6,
+                                               1, FAKE, need_k, None) == -7
+    G = [FAKE] * 7
+    # dh_last (the 11th argument) and dh0 (the 20th) overlapping.
+    assert lib.mqc_ssm_fused_bwd_chunked(*P, None, FAKE, K, FAKE, H, *G[:4], FAKE, FAKE, FAKE,
+                                         H, b, T, d, k, Lk, 1e-6, 1, FAKE, need_k, None) == -7
+
+
+def test_auto_chunk_count_within_the_launch_limit():
+    """The library's chunk length keeps batch * n_chunks within the chunked
+    launches' 65535 rows, also for large batches of few states."""
+    lib = nat.load()
+    for b, T, d, k in ((8192, 4096, 4, 1), (4096, 2048, 1, 2), (65535, 512, 1, 1),
+                       (1, 262144, 8, 64), (300, 100000, 1, 1)):
+        L = lib.mqc_ssm_chunk_len_auto(b, T, d, k, 1)
+        assert 1 <= L <= T
+        assert b * -(-T // L) <= 65535 or L == T, (b, T, d, k, L)
+        if L < T:
+            assert lib.mqc_ssm_chunked_workspace_bytes(b, T, d, k, L) > 0
 
 
 def test_gemm_validation_without_gpu():
@@ -502,19 +547,20 @@ def test_chunked_walks_check_before_any_launch():
     odd = ctypes.c_void_p(4096 + 2)  # 2-byte aligned: too little for 8-byte B loads
     big = 1 << 40
     # Inference: (delta, s, B, C, la, li, D, h0, y, h_last, batch, T, d, S, L, eps, dtype, ws, bytes, stream)
-    P = [FAKE, FAKE, odd] + [FAKE] * 7
+    # (h0 NULL: a chunked walk refuses h_last over h0.)
+    P = [FAKE, FAKE, odd] + [FAKE] * 4 + [None, FAKE, FAKE]
     assert lib.mqc_ssm_fused_fwd_chunked(*P, 1, 200, 8, 64, 64, 1e-6, bf, FAKE, big, None) == -4
-    P = [FAKE] * 10
+    P = [FAKE] * 7 + [None, FAKE, FAKE]
     # 2^22 d's x 64 states x 4 x 2 bytes = 2 GiB per (b, t) slice: past the 32-bit offsets.
     assert lib.mqc_ssm_fused_fwd_chunked(*P, 1, 200, 1 << 22, 64, 64, 1e-6, bf, FAKE, big, None) == -5
     # Training forward: 11 pointers (… h_last, h_ckpt), then ckpt_every.
-    P = [FAKE, FAKE, odd] + [FAKE] * 8
+    P = [FAKE, FAKE, odd] + [FAKE] * 4 + [None] + [FAKE] * 3
     assert lib.mqc_ssm_fused_fwd_train_chunked(*P, K, 1, 200, 8, 64, 64, 1e-6, bf, FAKE, big, None) == -4
     # Backward: 9 pointers, ckpt_every, 10 pointers (gy first).
     Q = [FAKE] * 9
-    R = [odd] + [FAKE] * 9
+    R = [odd] + [FAKE] * 8 + [None]  # dh0 NULL (it may not overlap dh_last)
     assert lib.mqc_ssm_fused_bwd_chunked(*Q, K, *R, 1, 200, 8, 64, 64, 1e-6, bf, FAKE, big, None) == -4
-    R = [FAKE] * 10
+    R = [FAKE] * 9 + [None]
     assert lib.mqc_ssm_fused_bwd_chunked(*Q, K, *R, 1, 200, 1 << 22, 64, 64, 1e-6, bf, FAKE, big,
                                          None) == -5
 

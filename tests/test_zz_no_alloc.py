@@ -65,6 +65,40 @@ def test_noalloc_matches_workspace_entry_point():
         assert_close(y_na, y_whole, 2e-2, f"noalloc vs whole walk {shape}")
 
 
+def test_noalloc_replays_in_a_hip_graph():
+    """The use the entry point is for: captured into a HIP graph (after
+    mqc_ssm_noalloc_prepare, so the capture records kernel launches only) and
+    replayed, with eager work between the replays, each replay equal to the
+    workspace entry point on the same inputs."""
+    lib = nat.load()
+    assert lib.mqc_ssm_noalloc_prepare() == 0
+    b, T, d, k, L = 1, 384, 128, 64, 64
+    print(f"noalloc graph case {(b, T, d, k)} L={L}", flush=True)
+    ins = _inputs(b, T, d, k, seed=11)
+    y_ws, h_ws = _run(lib, "mqc_ssm_fused_fwd_chunked", ins, L, True)
+    delta, s, Bm, C, la, li, D, h0 = ins
+    y = torch.empty(b, T, d, 4, device=DEV, dtype=Bm.dtype)
+    h = torch.empty(b, d, k, 4, device=DEV, dtype=torch.float32)
+    ptrs = [t.data_ptr() for t in (delta, s, Bm, C, la, li, D, h0, y, h)]
+    graph = torch.cuda.CUDAGraph()
+    status = []
+    with torch.cuda.graph(graph):
+        stream = torch.cuda.current_stream().cuda_stream
+        status.append(lib.mqc_ssm_fused_fwd_chunked_noalloc(*ptrs, b, T, d, k, L, 1e-6,
+                                                            nat.BF16, stream))
+    assert status == [0], status
+    for rep in range(3):
+        y.fill_(float("nan"))
+        h.fill_(float("nan"))
+        # Eager use of the same scratch between replays (another shape).
+        _run(lib, "mqc_ssm_fused_fwd_chunked_noalloc", _inputs(2, 200, 64, 32, seed=rep), 70,
+             False)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ws), f"replay {rep}: y differs"
+        assert torch.equal(h, h_ws), f"replay {rep}: h_last differs"
+
+
 def test_noalloc_refuses_more_than_its_scratch():
     lib = nat.load()
     b, T, d, k, L = 4, 4096, 2048, 64, 64
