@@ -1,7 +1,7 @@
 """Benchmark: QuaternionMamba2Block forward on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
-                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_train|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|decode|decode_graph|block_long|train|copy]
+                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_train|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|fused_bc|bc_unfused|decode|decode_graph|block_long|train|copy]
                     [--preset small|base|large]
 
 Workload (BASELINE configs[2]/[3] shape): one QuaternionMamba2Block forward,
@@ -714,6 +714,28 @@ def run_kernel_loop(args):
             x = torch.randn(B * T, DI, generator=g, device="cuda").to(bf)
             w = (torch.randn(DI * DS * 4, DI, generator=g, device="cuda") * 0.02).to(bf)
             fn = lambda: wide_linear(x, w)
+            nbytes = 0
+        elif args.mode in ("fused_bc", "bc_unfused"):
+            # Config 3's B/C projections and SSM: fused in one launch
+            # (mqc_ssm_fused_bc_fwd), or the block's unfused path (hipBLASLt GEMMs
+            # in column blocks, then mqc_ssm_fused_fwd), on the same operands.
+            from mambaqc_amd.layers.quaternion_linear import wide_linear
+            bf = torch.bfloat16
+            x = torch.randn(B, T, DI, generator=g, device="cuda").to(bf)
+            wb = (torch.randn(DI * DS * 4, DI, generator=g, device="cuda") * 0.02).to(bf)
+            wc = (torch.randn(DI * DS * 4, DI, generator=g, device="cuda") * 0.02).to(bf)
+            delta = torch.nn.functional.softplus(torch.randn(B, T, DI, generator=g, device="cuda") - 2).to(bf)
+            s = torch.randn(B, T, DI, generator=g, device="cuda").to(bf)
+            la = torch.randn(DI, DS, generator=g, device="cuda") * 0.5 + 1
+            li = torch.randn(DI, DS, 3, generator=g, device="cuda") * 0.1
+            Dv = torch.ones(DI, device="cuda")
+            if args.mode == "fused_bc":
+                fn = lambda: K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, Dv)
+            else:
+                def fn():
+                    Bq = wide_linear(x, wb).view(B, T, DI, DS, 4)
+                    Cq = wide_linear(x, wc).view(B, T, DI, DS, 4)
+                    return K.ssm_forward_fused_dl(delta, s, Bq, Cq, la, li, Dv)
             nbytes = 0
         elif args.mode == "copy":
             src = torch.empty(1 << 28, device="cuda")  # 1 GiB

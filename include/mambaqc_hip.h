@@ -194,6 +194,24 @@ int64_t mqc_ssm_chunked_scratch_bytes(void);
  * in the reference. */
 int mqc_ssm_noalloc_prepare(void);
 
+/* The block's B and C projections fused with its SSM (mqc_ssm_fused_fwd) in one
+ * launch, bf16 only (dtype MQC_BF16): B = x . B_weight^T and C = x . C_weight^T,
+ * viewed as [batch, seq_len, d_inner, d_state, 4], are computed 256 tokens at a time
+ * by MFMA tiles in LDS, rounded to bf16 as the unfused projections store them, and
+ * walked there, so neither is ever written to memory. x: [batch, seq_len, d_inner]
+ * (the projections' input, 16-byte aligned); B_weight, C_weight: [d_inner * d_state * 4,
+ * d_inner] (nn.Linear layout, 16-byte aligned); delta, s: [batch, seq_len, d_inner];
+ * the parameters, h0, y and h_last as in mqc_ssm_fused_fwd (y 8-byte aligned, h0 and
+ * h_last 16-byte aligned; h_last may be h0). d_inner a multiple of 64; d_state even,
+ * at most 64. Replaces B_proj/C_proj (F.linear, mambaqc/layers/quaternion_linear.py:145-161,
+ * called at mambaqc/models/quaternion_mamba2_block.py:186-191) together with the SSM
+ * they feed (quaternion_mamba2_block.py:206-228). */
+int mqc_ssm_fused_bc_fwd(const void* x, const void* B_weight, const void* C_weight,
+                         const void* delta, const void* s, const float* lambda_alpha,
+                         const float* lambda_imag, const float* D, const void* h0, void* y,
+                         void* h_last, int64_t batch, int64_t seq_len, int64_t d_inner,
+                         int64_t d_state, float eps, int dtype, void* stream);
+
 /* C[M, N] = X[M, K] . W[N, K]^T in bf16 with fp32 accumulation (dtype must be
  * MQC_BF16), contiguous row-major X, W, C, 16-byte aligned; N a multiple of
  * 256, K of 64, M any. The hand-written MFMA GEMM of the block's B/C

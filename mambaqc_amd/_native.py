@@ -69,6 +69,8 @@ SIGNATURES = {
     "mqc_ssm_fused_fwd_chunked_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                           _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp],
     "mqc_ssm_noalloc_prepare": [],
+    "mqc_ssm_fused_bc_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                             _i64, _i64, _i64, _i64, _f32, _int, _vp],
 }
 
 # name -> argtypes of the entry points that return int64_t (a size, or a

@@ -9,25 +9,8 @@
 // measured against hipBLASLt on the same shapes; the block keeps hipBLASLt,
 // which is faster at the config-3 shape (M 8192, N 393216, K 1536).
 //
-// Tiling (gfx950):
-//   - 256 x 256 output tile per workgroup of 8 waves (two per SIMD); wave w owns 128 columns
-//     (w >> 2) x 64 rows (w & 3) as 8 x 4 blocks of v_mfma_f32_16x16x32_bf16 accumulators
-//     (128 fp32 per lane). W rows are the MFMA's first operand and X rows its second, so
-//     each lane ends with 4 consecutive output columns of one row per 16 x 16 block. On
-//     random operands the 16 x 16 x 32 shape sustains more than the 32 x 32 x 16 one:
-//     measured with operands held in registers, 2098 against 1785 TFLOP/s (both about
-//     2400 on zeros: the MFMA rate depends on the operand data through the chip's power).
-//   - K in steps of 64 through two LDS stages of 64 KB (X and W tiles of 256 rows x 128
-//     bytes), filled by global_load_lds_dwordx4 (16 bytes per lane straight into LDS) in its
-//     scalar-base form: each DMA instruction covers 8 rows whose base address is
-//     wave-uniform (SGPRs), and a lane adds one of two 32-bit offsets (the swizzle below
-//     depends on the row group's parity only), so the loads take 2 VGPRs instead of a
-//     64-bit pointer per instruction. The 16-byte chunk c of row r is stored at chunk
-//     c ^ ((r >> 1) & 7), so the 16 rows one ds_read_b128 group reads fall on distinct banks.
-//   - One barrier per K step: after it, the stage consumed before it is free and receives
-//     the loads of the next step, which then run during this step's MFMAs. The fragments
-//     of the step's second K slice are read while the first slice's MFMAs issue, one read
-//     after each MFMA.
+// Tiling (gfx950): the 256 x 256 MFMA main loop of mfma_tile.hpp (8 waves, two 64 KB
+// LDS stages filled by global->LDS DMA, 16 x 16 x 32 bf16 MFMAs), plus:
 //   - Tiles in launch order with the M tile fastest: the 256 tiles in flight cover all of X
 //     (in the Infinity Cache) and a few W tiles, each of which is read from HBM about once.
 //   - Epilogue through LDS: the tile is written to LDS in the MFMA layout (rows of 512 bytes,
@@ -37,55 +20,17 @@
 // free; N must be a multiple of 256 and K of 64.
 #include <atomic>
 
-#include "common.hpp"
+#include "mfma_tile.hpp"
 
 namespace mqc {
 namespace {
 
-typedef __bf16 gbf16x8 __attribute__((ext_vector_type(8)));
-typedef float gfloatx4 __attribute__((ext_vector_type(4)));
-typedef unsigned int gu32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned int gu32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void_t;
+using namespace mfma;
 
-constexpr int kGT = 256;                   // tile rows and columns
-constexpr int kGBK = 64;                   // K per stage
-constexpr int kGThreads = 512;             // 8 waves
-constexpr int kRowBytes = kGBK * 2;        // 128 bytes of a tile row per stage
-constexpr int kTileBytes = kGT * kRowBytes;    // 32 KB
-constexpr int kStageBytes = 2 * kTileBytes;    // X and W tiles
-constexpr int kLdsBytes = 2 * kStageBytes;     // two stages = 128 KB (also the epilogue tile)
-constexpr int kRowsPerLoad = 64 * 16 / kRowBytes;        // 8 rows per DMA instruction
-constexpr int kLoads = kGT / kRowsPerLoad / 8;           // 4 per wave per operand per stage
-constexpr int kWB = 8;                     // 16-row W blocks per wave
-constexpr int kXB = 4;                     // 16-row X blocks per wave
-
-// 16 bytes per lane from global memory (sbase + voff, sbase wave-uniform) into LDS at
-// lds_addr + lane * 16. The kernel waits for these with explicit s_waitcnt vmcnt; issued
-// as inline assembly because the compiler, unable to tell the two stages apart, would
-// otherwise wait for every load in flight before each LDS read. M0 is set here; nothing
-// else in this kernel uses it.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"  // M0 in the clobber list, as intended
-__device__ inline void dma16(const void* sbase, uint32_t voff, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(voff), "s"(sbase), "s"(lds_addr) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-__device__ inline int gswz(int row, int c) { return c ^ ((row >> 1) & 7); }
-
-__device__ inline uint32_t pk_bf16(float a, float b) {
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 h16x2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, h16x2));
-}
-
-// s_waitcnt vmcnt(N) with expcnt and lgkmcnt at their maxima (gfx9 fields).
-template <int N>
-__device__ inline void wait_vmcnt() {
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
+constexpr int kGT = kT;
+constexpr int kGBK = kBK;
+constexpr int kGThreads = kThreads;
+constexpr int kLdsBytes = kStagesBytes;  // two stages = 128 KB (also the epilogue tile)
 
 // One 256 x 256 tile. FULL_M: all 256 rows of the tile exist (every row tile but a
 // ragged last one, whose rows past M read row M - 1).
@@ -96,98 +41,32 @@ __device__ inline void gemm_tile(const __bf16* __restrict__ X, const __bf16* __r
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-
-  // DMA instruction i of this wave carries tile rows (wave * kLoads + i) * 8 + lrow, lane
-  // chunk (lane % 8) ^ swizzle; the swizzle depends on the parity of i only.
-  const int lrow = lane >> 3;
-  const int lslot = lane & 7;
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)lds;
-  uint32_t voff[2], cbyte[2];
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    cbyte[p] = (uint32_t)((lslot ^ ((p * 4 + (lrow >> 1)) & 7)) * 16);
-    voff[p] = (uint32_t)(lrow * K * 2) + cbyte[p];
-  }
-  auto issue_stage = [&](int kt) {
-    const int k0 = kt * kGBK;
-    const uint32_t sb = lds0 + (uint32_t)((kt & 1) * kStageBytes);
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int g = (wave * kLoads + i) * kRowsPerLoad;
-      const uint32_t off = (uint32_t)((wave * kLoads + i) * 1024);
-      dma16(W + ((int64_t)(n0 + g) * K + k0), voff[i & 1], sb + off);
-      if constexpr (FULL_M) {
-        dma16(X + ((int64_t)(m0 + g) * K + k0), voff[i & 1], sb + kTileBytes + off);
-      } else {
-        // The last row tile: rows past M read row M - 1.
-        const int gb = m0 + g < M ? m0 + g : M - 1;
-        const int r = m0 + g + lrow < M ? m0 + g + lrow : M - 1;
-        dma16(X + ((int64_t)gb * K + k0), (uint32_t)((r - gb) * K * 2) + cbyte[i & 1],
-              sb + kTileBytes + off);
-      }
-    }
-  };
-
   const int wn = wave >> 2;
   const int wm = wave & 3;
-  const int rl = lane & 15;  // row within a 16-row block
-  const int q = lane >> 4;   // 16-byte chunk within a 32-wide K slice
-  gfloatx4 acc[kWB][kXB];
+  const int rl = lane & 15;
+  const int q = lane >> 4;
+  floatx4 acc[kWB][kXB];
 #pragma unroll
   for (int a = 0; a < kWB; ++a)
 #pragma unroll
-    for (int b = 0; b < kXB; ++b) acc[a][b] = (gfloatx4){};
-  // LDS byte offsets of this lane's fragments per K slice; the blocks of a wave are
-  // 16 rows apart, which keeps the swizzle, so they add constants.
-  int woff[2], xoff[2];
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    const int c = 4 * kk + q;
-    const int rw = wn * 128 + rl;
-    woff[kk] = rw * kRowBytes + gswz(rw, c) * 16;
-    const int rx = wm * 64 + rl;
-    xoff[kk] = kTileBytes + rx * kRowBytes + gswz(rx, c) * 16;
-  }
-  gbf16x8 wf[2][kWB], xf[2][kXB];
-  auto read_frags = [&](int buf, const char* sb, int kk) {
-#pragma unroll
-    for (int nb = 0; nb < kWB; ++nb) wf[buf][nb] = *(const gbf16x8*)(sb + woff[kk] + nb * 16 * kRowBytes);
-#pragma unroll
-    for (int mb = 0; mb < kXB; ++mb) xf[buf][mb] = *(const gbf16x8*)(sb + xoff[kk] + mb * 16 * kRowBytes);
-  };
-  auto mfmas = [&](int buf) {
-#pragma unroll
-    for (int nb = 0; nb < kWB; ++nb)
-#pragma unroll
-      for (int mb = 0; mb < kXB; ++mb)
-        acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[buf][nb], xf[buf][mb], acc[nb][mb], 0, 0, 0);
-  };
-
-  const int KT = K / kGBK;
-  issue_stage(0);
-  for (int kt = 0; kt < KT; ++kt) {
-    // This wave's loads of stage kt are the only ones in flight.
-    wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
-    if (kt + 1 < KT) issue_stage(kt + 1);
-    const char* sbase = lds + (kt & 1) * kStageBytes;
-    read_frags(0, sbase, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    // First K slice: its MFMAs with the second slice's fragment reads, one after each MFMA.
-    read_frags(1, sbase, 1);
-    mfmas(0);
-#pragma unroll
-    for (int g = 0; g < kWB + kXB; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    for (int b = 0; b < kXB; ++b) acc[a][b] = (floatx4){};
+  auto wrow = [&](int g, int k0) -> const void* { return W + ((int64_t)(n0 + g) * K + k0); };
+  auto xrow = [&](int g, int k0, int i, uint32_t& voff, const DmaLane& dl) -> const void* {
+    if constexpr (FULL_M) {
+      voff = (uint32_t)(dl.lrow * K * 2) + dl.cbyte[i & 1];
+      return X + ((int64_t)(m0 + g) * K + k0);
+    } else {
+      // The last row tile: rows past M read row M - 1.
+      const int gb = m0 + g < M ? m0 + g : M - 1;
+      const int r = m0 + g + dl.lrow < M ? m0 + g + dl.lrow : M - 1;
+      voff = (uint32_t)((r - gb) * K * 2) + dl.cbyte[i & 1];
+      return X + ((int64_t)gb * K + k0);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(1);
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  };
+  tile_kloop(K, K, lds, acc, wrow, xrow);
 
   // Epilogue through LDS (every wave is past its last LDS read at the barrier).
-  __builtin_amdgcn_s_waitcnt(0xC07F);
+  wait_lgkm0();
   __builtin_amdgcn_s_barrier();
 #pragma unroll
   for (int nb = 0; nb < kWB; ++nb)
@@ -195,20 +74,20 @@ __device__ inline void gemm_tile(const __bf16* __restrict__ X, const __bf16* __r
     for (int mb = 0; mb < kXB; ++mb) {
       const int ml = wm * 64 + mb * 16 + rl;
       const int nl = wn * 128 + nb * 16 + 4 * q;
-      const gfloatx4& v = acc[nb][mb];
-      const gu32x2 pk = {pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])};
-      *(gu32x2*)(lds + ml * 512 + ((nl >> 3) ^ (ml & 31)) * 16 + (nl & 7) * 2) = pk;
+      const floatx4& v = acc[nb][mb];
+      const u32x2 pk = {pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])};
+      *(u32x2*)(lds + ml * 512 + ((nl >> 3) ^ (ml & 31)) * 16 + (nl & 7) * 2) = pk;
     }
-  __builtin_amdgcn_s_waitcnt(0xC07F);
+  wait_lgkm0();
   __builtin_amdgcn_s_barrier();
   const int hi = lane >> 5;
   const int l32 = lane & 31;
 #pragma unroll
   for (int i = 0; i < kGT / 16; ++i) {
     const int row = (i * 8 + wave) * 2 + hi;
-    const gu32x4 v = *(const gu32x4*)(lds + row * 512 + ((l32 ^ (row & 31)) * 16));
+    const u32x4 v = *(const u32x4*)(lds + row * 512 + ((l32 ^ (row & 31)) * 16));
     if (FULL_M || m0 + row < M)
-      __builtin_nontemporal_store(v, (gu32x4*)(C + (int64_t)(m0 + row) * N + n0 + l32 * 8));
+      __builtin_nontemporal_store(v, (u32x4*)(C + (int64_t)(m0 + row) * N + n0 + l32 * 8));
   }
 }
 

@@ -1,0 +1,181 @@
+#pragma once
+// The MFMA main loop shared by the library's bf16 GEMM tiles (gfx950):
+//   acc += W_tile[256 rows, K] . X_tile[256 rows, K]^T
+// for one 256 x 256 output tile, fp32 accumulation.
+//
+//   - 8 waves (two per SIMD); wave w owns W rows (w >> 2) * 128 + [0, 128) and X rows
+//     (w & 3) * 64 + [0, 64) as 8 x 4 blocks of v_mfma_f32_16x16x32_bf16 accumulators
+//     (128 fp32 per lane). W rows are the MFMA's first operand and X rows its second, so
+//     in block (nb, mb) lane l holds the 4 consecutive W rows
+//     (w >> 2) * 128 + nb * 16 + 4 * (l >> 4) + [0, 4) of X row (w & 3) * 64 + mb * 16 +
+//     (l & 15). On random operands the 16 x 16 x 32 shape sustains more than the
+//     32 x 32 x 16 one: measured with operands held in registers, 2098 against
+//     1785 TFLOP/s (both about 2400 on zeros: the MFMA rate depends on the operand data
+//     through the chip's power).
+//   - K in steps of 64 through two LDS stages of 64 KB (X and W tiles of 256 rows x 128
+//     bytes), filled by global_load_lds_dwordx4 (16 bytes per lane straight into LDS) in
+//     its scalar-base form: each DMA instruction covers 8 rows whose base address is
+//     wave-uniform (SGPRs), and a lane adds a 32-bit offset, so the loads take one VGPR
+//     each instead of a 64-bit pointer. The 16-byte chunk c of row r is stored at chunk
+//     c ^ ((r >> 1) & 7), so the 16 rows one ds_read_b128 group reads fall on distinct
+//     banks.
+//   - One barrier per K step: after it, the stage consumed before it is free and receives
+//     the loads of the next step, which then run during this step's MFMAs. The fragments
+//     of the step's second K slice are read while the first slice's MFMAs issue, one read
+//     after each MFMA.
+#include "common.hpp"
+
+namespace mqc {
+namespace mfma {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int kT = 256;                   // tile rows and columns
+constexpr int kBK = 64;                   // K per stage
+constexpr int kThreads = 512;             // 8 waves
+constexpr int kRowBytes = kBK * 2;        // 128 bytes of a tile row per stage
+constexpr int kTileBytes = kT * kRowBytes;     // 32 KB
+constexpr int kStageBytes = 2 * kTileBytes;    // X and W tiles
+constexpr int kStagesBytes = 2 * kStageBytes;  // two stages = 128 KB
+constexpr int kRowsPerLoad = 64 * 16 / kRowBytes;  // 8 rows per DMA instruction
+constexpr int kLoads = kT / kRowsPerLoad / 8;      // 4 per wave per operand per stage
+constexpr int kWB = 8;                    // 16-row W blocks per wave
+constexpr int kXB = 4;                    // 16-row X blocks per wave
+
+// 16 bytes per lane from global memory (sbase + voff, sbase wave-uniform) into LDS at
+// lds_addr + lane * 16. The kernel waits for these with explicit s_waitcnt vmcnt; issued
+// as inline assembly because the compiler, unable to tell the two stages apart, would
+// otherwise wait for every load in flight before each LDS read. M0 is set here; nothing
+// else in these kernels uses it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 in the clobber list, as intended
+__device__ inline void dma16(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds_addr) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ inline int gswz(int row, int c) { return c ^ ((row >> 1) & 7); }
+
+__device__ inline uint32_t pk_bf16(float a, float b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 h16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, h16x2));
+}
+
+// s_waitcnt vmcnt(N) with expcnt and lgkmcnt at their maxima (gfx9 fields).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// s_waitcnt lgkmcnt(0) (LDS and scalar memory) with vmcnt and expcnt at their maxima.
+__device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Per-lane DMA geometry: DMA instruction i of a wave carries tile rows
+// (wave * kLoads + i) * 8 + lrow(), 16-byte chunk lslot() ^ swizzle; the swizzle
+// depends on the parity of i only, so a lane needs two chunk offsets.
+struct DmaLane {
+  int lrow;
+  uint32_t cbyte[2];
+  __device__ explicit DmaLane(int lane) : lrow(lane >> 3) {
+    const int lslot = lane & 7;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) cbyte[p] = (uint32_t)((lslot ^ ((p * 4 + (lrow >> 1)) & 7)) * 16);
+  }
+};
+
+// The K loop of one tile into acc (which it does not clear). For DMA instruction i of
+// this wave (tile rows g .. g + 7, g = (wave * kLoads + i) * 8) and K offset k0 (in
+// elements):
+//   wrow(g, k0)           -> wave-uniform pointer to W's row g, column k0; the lane reads
+//                            row g + lrow at byte offset lrow * ld_w * 2 + cbyte;
+//   xrow(g, k0, i, voff)  -> wave-uniform pointer for X's rows, with the lane's byte
+//                            offset from it written to voff (the caller may clamp rows).
+// Returns after the last MFMA; the caller waits on lgkmcnt and barriers before reusing
+// the LDS stages.
+template <typename WRow, typename XRow>
+__device__ inline void tile_kloop(int K, int ld_w, char* lds, floatx4 (&acc)[kWB][kXB],
+                                  const WRow& wrow, const XRow& xrow) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const DmaLane dl(lane);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)lds;
+  uint32_t wvoff[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) wvoff[p] = (uint32_t)(dl.lrow * ld_w * 2) + dl.cbyte[p];
+  auto issue_stage = [&](int kt) {
+    const int k0 = kt * kBK;
+    const uint32_t sb = lds0 + (uint32_t)((kt & 1) * kStageBytes);
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int g = (wave * kLoads + i) * kRowsPerLoad;
+      const uint32_t off = (uint32_t)((wave * kLoads + i) * 1024);
+      dma16(wrow(g, k0), wvoff[i & 1], sb + off);
+      uint32_t xv;
+      const void* xb = xrow(g, k0, i, xv, dl);
+      dma16(xb, xv, sb + kTileBytes + off);
+    }
+  };
+
+  const int wn = wave >> 2;
+  const int wm = wave & 3;
+  const int rl = lane & 15;  // row within a 16-row block
+  const int q = lane >> 4;   // 16-byte chunk within a 32-wide K slice
+  // LDS byte offsets of this lane's fragments per K slice; the blocks of a wave are
+  // 16 rows apart, which keeps the swizzle, so they add constants.
+  int woff[2], xoff[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const int c = 4 * kk + q;
+    const int rw = wn * 128 + rl;
+    woff[kk] = rw * kRowBytes + gswz(rw, c) * 16;
+    const int rx = wm * 64 + rl;
+    xoff[kk] = kTileBytes + rx * kRowBytes + gswz(rx, c) * 16;
+  }
+  bf16x8 wf[2][kWB], xf[2][kXB];
+  auto read_frags = [&](int buf, const char* sb, int kk) {
+#pragma unroll
+    for (int nb = 0; nb < kWB; ++nb) wf[buf][nb] = *(const bf16x8*)(sb + woff[kk] + nb * 16 * kRowBytes);
+#pragma unroll
+    for (int mb = 0; mb < kXB; ++mb) xf[buf][mb] = *(const bf16x8*)(sb + xoff[kk] + mb * 16 * kRowBytes);
+  };
+  auto mfmas = [&](int buf) {
+#pragma unroll
+    for (int nb = 0; nb < kWB; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < kXB; ++mb)
+        acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[buf][nb], xf[buf][mb], acc[nb][mb], 0, 0, 0);
+  };
+
+  const int KT = K / kBK;
+  issue_stage(0);
+  for (int kt = 0; kt < KT; ++kt) {
+    // This wave's loads of stage kt are the only ones in flight.
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (kt + 1 < KT) issue_stage(kt + 1);
+    const char* sbase = lds + (kt & 1) * kStageBytes;
+    read_frags(0, sbase, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // First K slice: its MFMAs with the second slice's fragment reads, one after each MFMA.
+    read_frags(1, sbase, 1);
+    mfmas(0);
+#pragma unroll
+    for (int g = 0; g < kWB + kXB; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+}  // namespace mfma
+}  // namespace mqc

@@ -479,3 +479,67 @@ def ssm_forward_front_dl(dt_raw: torch.Tensor, g_raw: torch.Tensor, x: torch.Ten
     delta, s = ssm_front(dt_raw, g_raw, x)
     return ssm_forward_fused_dl(delta, s, B, C, lambda_alpha, lambda_imag, D, eps=eps, h0=h0,
                                 return_state=return_state)
+
+
+# --- B/C projections fused with the walk (inference) ---------------------------
+
+def fused_bc_eligible(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torch.Tensor,
+                      d_state: int) -> bool:
+    """Whether ssm_forward_fused_bc takes these operands: bf16 x [batch, T, d_inner]
+    with d_inner a multiple of 64, bf16 weights [d_inner * d_state * 4, d_inner] of
+    one shape, d_state even and at most 64, all on a ROCm device."""
+    if x.dim() != 3 or not (x.is_cuda and B_weight.is_cuda and C_weight.is_cuda):
+        return False
+    d_inner = x.shape[-1]
+    return (x.dtype == B_weight.dtype == C_weight.dtype == torch.bfloat16
+            and d_inner % 64 == 0 and 0 < d_state <= 64 and d_state % 2 == 0
+            and tuple(B_weight.shape) == tuple(C_weight.shape) == (d_inner * d_state * 4, d_inner))
+
+
+def ssm_forward_fused_bc(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torch.Tensor,
+                         delta: torch.Tensor, s: torch.Tensor, lambda_alpha: torch.Tensor,
+                         lambda_imag: torch.Tensor, D: torch.Tensor, eps: float = 1e-6,
+                         h0: torch.Tensor | None = None, return_state: bool = False):
+    """The block's B/C projections and its SSM in one HIP launch (inference, bf16).
+
+    B = x B_weight^T and C = x C_weight^T, as [batch, seq_len, d_inner, d_state, 4]
+    (the bias-free real -> quaternion projections,
+    mambaqc/layers/quaternion_linear.py:145-161), are computed 256 tokens at a time
+    on chip, rounded to bf16 as the projections would store them, and walked there
+    by ssm_forward_fused_dl's recurrence; neither is ever written to memory.
+    x: [batch, seq_len, d_inner] bf16 (the projections' input); B_weight, C_weight:
+    [d_inner * d_state * 4, d_inner] bf16; delta, s, the Lambda parameters, D and h0
+    as in ssm_forward_fused_dl. Returns y [batch, seq_len, d_inner, 4] bf16 (and the
+    final fp32 state if return_state). Inference only (no autograd).
+    """
+    batch, T, d_inner = x.shape
+    d_state = lambda_alpha.shape[-1] if lambda_alpha.dim() == 2 else 0
+    assert delta.shape == (batch, T, d_inner) and s.shape == (batch, T, d_inner)
+    assert lambda_alpha.shape == (d_inner, d_state)
+    assert lambda_imag.shape == (d_inner, d_state, 3)
+    assert D.shape == (d_inner,)
+    if h0 is not None:
+        assert h0.shape == (batch, d_inner, d_state, 4)
+    nat.require_device("ssm_forward_fused_bc", x, B_weight, C_weight, delta, s, lambda_alpha,
+                       lambda_imag, D)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (
+            x, B_weight, C_weight, delta, s, lambda_alpha, lambda_imag, D)):
+        raise RuntimeError("ssm_forward_fused_bc: inference only; run under torch.no_grad")
+    if not fused_bc_eligible(x, B_weight, C_weight, d_state):
+        raise ValueError("ssm_forward_fused_bc: needs bf16 x [batch, T, d_inner] with d_inner a "
+                         "multiple of 64, bf16 weights [d_inner * d_state * 4, d_inner] and an "
+                         "even d_state <= 64")
+    bf = torch.bfloat16
+    xc, wb, wc = (nat.aligned16(t.detach()) for t in (x, B_weight, C_weight))
+    dl, sv = (nat.aligned16(t.detach().to(bf)) for t in (delta, s))
+    la, li, Dv = (nat.param_f32(t) for t in (lambda_alpha, lambda_imag, D))
+    h0c = None if h0 is None else nat.aligned16(h0.detach().float())
+    y = torch.empty(batch, T, d_inner, 4, device=x.device, dtype=bf)
+    h_last = (torch.empty(batch, d_inner, d_state, 4, device=x.device, dtype=torch.float32)
+              if return_state else None)
+    nat.call("mqc_ssm_fused_bc_fwd", xc, xc.data_ptr(), wb.data_ptr(), wc.data_ptr(),
+             dl.data_ptr(), sv.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(),
+             nat.ptr(h0c), y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state,
+             float(eps), nat.BF16, nat.stream_of(xc))
+    return (y, h_last) if return_state else y
+

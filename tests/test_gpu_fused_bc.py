@@ -1,0 +1,158 @@
+"""GPU parity of the fused B/C projections + SSM walk (mqc_ssm_fused_bc_fwd,
+kernels.ssm_forward_fused_bc) against the CPU oracle and against the unfused
+path (torch's GEMMs for B and C, then mqc_ssm_fused_fwd).
+
+The oracle side: B = x W_B^T and C = x W_C^T in fp32 from the same bf16
+operands, rounded to bf16 (the dtype the projections store and the fused kernel
+rounds to on chip), then oracle.ssm_forward_dl_reference in float64. bf16
+tolerance 2e-2 with the atol floor of rtol * max|ref| (conftest.assert_close).
+"""
+import ctypes
+
+import pytest
+import torch
+
+import oracle
+from conftest import assert_close
+
+from mambaqc_amd import _native as nat
+from mambaqc_amd import kernels as K
+from mambaqc_amd.kernels.ssm_fused import fused_bc_eligible
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+def _inputs(b, T, d, k, seed, w_std=None):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g, device=DEV)
+    w_std = 0.3 / d ** 0.5 if w_std is None else w_std
+    x = r(b, T, d).to(BF)
+    wb = (r(d * k * 4, d) * w_std).to(BF)
+    wc = (r(d * k * 4, d) * w_std).to(BF)
+    delta = torch.nn.functional.softplus(r(b, T, d) - 1).to(BF)
+    s = r(b, T, d).to(BF)
+    la = r(d, k) * 0.5 + 1
+    li = r(d, k, 3) * 0.3
+    D = 1 + 0.1 * r(d)
+    h0 = r(b, d, k, 4) * 0.2
+    return x, wb, wc, delta, s, la, li, D, h0
+
+
+def _bc_rounded(x, w, d_slice, k):
+    """B (or C) for the d's of d_slice, as the projections store it: fp32 GEMM of
+    the bf16 operands, rounded to bf16; [b, T, n_d, k, 4] in float64 on the CPU."""
+    b, T, d = x.shape
+    rows = w.view(d, k * 4, d)[d_slice].reshape(-1, d)
+    out = (x.float().reshape(-1, d) @ rows.float().t()).to(BF)
+    return out.double().cpu().view(b, T, -1, k, 4)
+
+
+def _oracle(x, wb, wc, delta, s, la, li, D, h0, d_slice, b_slice=slice(None)):
+    k = la.shape[-1]
+    xs = x[b_slice]
+    Bq = _bc_rounded(xs, wb, d_slice, k)
+    Cq = _bc_rounded(xs, wc, d_slice, k)
+    up = lambda t: t.detach().double().cpu()
+    return oracle.ssm_forward_dl_reference(
+        up(delta[b_slice][:, :, d_slice]), up(s[b_slice][:, :, d_slice]), Bq, Cq,
+        up(la[d_slice]), up(li[d_slice]), up(D[d_slice]),
+        h0=None if h0 is None else up(h0[b_slice][:, d_slice]), return_state=True)
+
+
+@pytest.mark.parametrize("shape", [
+    (1, 256, 64, 64),    # one full tile, one K step
+    (2, 512, 128, 64),   # state carried across tiles
+    (3, 300, 192, 32),   # ragged last tile, one half of states, d_inner 3 x 64
+    (1, 77, 64, 16),     # shorter than a tile, a ragged half (16 states)
+    (2, 600, 64, 48),    # two halves, the second ragged
+    (1, 1, 128, 2),      # one token, two states
+])
+@pytest.mark.parametrize("with_h0", [False, True])
+def test_fused_bc_vs_oracle(shape, with_h0):
+    b, T, d, k = shape
+    print(f"fused_bc vs oracle {shape} h0={with_h0}", flush=True)
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=sum(shape))
+    h0 = h0 if with_h0 else None
+    assert fused_bc_eligible(x, wb, wc, k)
+    with torch.no_grad():
+        y, h = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0, return_state=True)
+    want_y, want_h = _oracle(x, wb, wc, delta, s, la, li, D, h0, slice(None))
+    assert y.dtype == BF and h.dtype == torch.float32
+    assert_close(y, want_y, 2e-2, f"fused y {shape}")
+    assert_close(h, want_h, 2e-2, f"fused h_last {shape}")
+
+
+def test_fused_bc_equals_unfused_path_small():
+    """Against the unfused path on the same weights (torch's bf16 GEMMs, then the
+    library's walk): the same recurrence on B and C that differ at most by the
+    rounding of differently ordered fp32 sums."""
+    b, T, d, k = 2, 700, 128, 64
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=5)
+    with torch.no_grad():
+        y, h = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0, return_state=True)
+        Bq = torch.nn.functional.linear(x, wb).view(b, T, d, k, 4)
+        Cq = torch.nn.functional.linear(x, wc).view(b, T, d, k, 4)
+        y2, h2 = K.ssm_forward_fused_dl(delta, s, Bq, Cq, la, li, D, h0=h0, return_state=True)
+    assert_close(y, y2, 2e-2, "fused vs unfused y")
+    assert_close(h, h2, 2e-2, "fused vs unfused h_last")
+
+
+def test_fused_bc_config3_full_size():
+    """Config 3's shape (B4 T2048 d_inner 1536 S64, bf16): the whole output
+    against the unfused path on the same weights, and d-slices in every batch row
+    (each (b, d) is its own workgroup; slices at both ends and in the middle of
+    the launch order) against the oracle."""
+    b, T, d, k = 4, 2048, 1536, 64
+    print("fused_bc config 3 full size", flush=True)
+    x, wb, wc, delta, s, la, li, D, _ = _inputs(b, T, d, k, seed=0, w_std=0.02)
+    with torch.no_grad():
+        y = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D)
+        Bq = torch.nn.functional.linear(x, wb).view(b, T, d, k, 4)
+        Cq = torch.nn.functional.linear(x, wc).view(b, T, d, k, 4)
+        y2 = K.ssm_forward_fused_dl(delta, s, Bq, Cq, la, li, D)
+        del Bq, Cq
+    assert_close(y, y2, 2e-2, "C3 fused vs unfused")
+    for b0, ds in ((0, slice(0, 2)), (1, slice(700, 702)), (2, slice(1000, 1001)),
+                   (3, slice(1534, 1536))):
+        want, _ = _oracle(x, wb, wc, delta, s, la, li, D, None, ds, slice(b0, b0 + 1))
+        assert_close(y[b0:b0 + 1, :, ds], want, 2e-2, f"C3 fused slice b={b0} d={ds}")
+
+
+def test_fused_bc_state_in_place_and_empty():
+    """h_last may be h0 (each (b, d) reads its own states before it writes them),
+    through the C ABI; an empty sequence copies h0 to h_last."""
+    b, T, d, k = 2, 300, 64, 64
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=9)
+    with torch.no_grad():
+        y_ref, h_ref = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0,
+                                              return_state=True)
+    lib = nat.load()
+    h = h0.clone()
+    y = torch.empty_like(y_ref)
+    stream = torch.cuda.current_stream().cuda_stream
+    st = lib.mqc_ssm_fused_bc_fwd(x.data_ptr(), wb.data_ptr(), wc.data_ptr(), delta.data_ptr(),
+                                  s.data_ptr(), la.data_ptr(), li.data_ptr(), D.data_ptr(),
+                                  h.data_ptr(), y.data_ptr(), h.data_ptr(), b, T, d, k, 1e-6,
+                                  nat.BF16, stream)
+    assert st == 0, nat.status_string(st)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref) and torch.equal(h, h_ref)
+    h_out = torch.full_like(h0, float("nan"))
+    st = lib.mqc_ssm_fused_bc_fwd(None, None, None, None, None, la.data_ptr(), li.data_ptr(),
+                                  D.data_ptr(), h0.data_ptr(), None, h_out.data_ptr(), b, 0, d,
+                                  k, 1e-6, nat.BF16, stream)
+    assert st == 0, nat.status_string(st)
+    torch.cuda.synchronize()
+    assert torch.equal(h_out, h0)
+
+
+def test_fused_bc_rejects_what_it_cannot_run():
+    x, wb, wc, delta, s, la, li, D, _ = _inputs(1, 16, 64, 4, seed=3)
+    assert not fused_bc_eligible(x.float(), wb.float(), wc.float(), 4)
+    assert not fused_bc_eligible(x, wb, wc, 3)
+    with pytest.raises(ValueError):
+        K.ssm_forward_fused_bc(x.float(), wb.float(), wc.float(), delta, s, la, li, D)
+    with pytest.raises(RuntimeError):
+        K.ssm_forward_fused_bc(x, wb.requires_grad_(), wc, delta, s, la, li, D)

@@ -29,7 +29,7 @@ def declared_symbols():
 
 def test_header_declares_the_api():
     names = declared_symbols()
-    assert len(names) == 33, names
+    assert len(names) == 34, names
     assert set(nat.SIGNATURES) | set(nat.SIGNATURES_I64) <= set(names)
 
 
@@ -229,6 +229,27 @@ def test_chunked_walks_refuse_in_place_state_without_gpu():
     # dh_last (the 11th argument) and dh0 (the 20th) overlapping.
     assert lib.mqc_ssm_fused_bwd_chunked(*P, None, FAKE, K, FAKE, H, *G[:4], FAKE, FAKE, FAKE,
                                          H, b, T, d, k, Lk, 1e-6, 1, FAKE, need_k, None) == -7
+
+
+def test_fused_bc_validation_without_gpu():
+    """mqc_ssm_fused_bc_fwd refuses, before any HIP call: a dtype other than bf16,
+    d_state odd or above 64, d_inner not a multiple of 64, NULL operands and
+    misaligned pointers; nothing to do is not an error."""
+    lib = nat.load()
+    bf = 1
+    odd = ctypes.c_void_p(4096 + 8)
+    P = [FAKE] * 8  # x, W_B, W_C, delta, s, lambda_alpha, lambda_imag, D
+    # (…, h0, y, h_last, batch, seq_len, d_inner, d_state, eps, dtype, stream)
+    assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, 1, 16, 64, 64, 1e-6, 0, None) == -3
+    assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, 1, 16, 64, 63, 1e-6, bf, None) == -2
+    assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, 1, 16, 64, 66, 1e-6, bf, None) == -5
+    assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, 1, 16, 96, 64, 1e-6, bf, None) == -2
+    assert lib.mqc_ssm_fused_bc_fwd(None, *P[1:], None, FAKE, None, 1, 16, 64, 64, 1e-6, bf,
+                                    None) == -1
+    assert lib.mqc_ssm_fused_bc_fwd(odd, *P[1:], None, FAKE, None, 1, 16, 64, 64, 1e-6, bf,
+                                    None) == -4
+    assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, 0, 16, 64, 64, 1e-6, bf, None) == 0
+    assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, -1, 16, 64, 64, 1e-6, bf, None) == -2
 
 
 def test_auto_chunk_count_within_the_launch_limit():
