@@ -13,8 +13,10 @@ accumulation in the HIP kernels, synthetic x ~ N(0, 1) resident in HBM.
 timed region bracketed by torch.cuda.synchronize()). `roofline` is the fused
 SSM kernel (mqc_ssm_fused_fwd): algorithmic bytes per launch divided by its
 mean launch duration, measured with HIP events on the stream it runs on.
-`roofline_gemm` puts the B projection GEMM (hipBLASLt, most of the block's
-time) against the dense bf16 MFMA peak, with this library's GEMM beside it.
+`roofline_gemm` puts the kernel that holds most of the block's time, the B/C
+projections fused with the SSM walk (mqc_ssm_fused_bc_fwd: both projections'
+flops per launch), against the dense bf16 MFMA peak, with hipBLASLt's and this
+library's standalone GEMMs of one projection beside it.
 `cpu_baseline` times the CPU oracle (a restatement of the reference's
 sequential torch path) on a bounded prefix of the same workload. `train_c4`
 reports config 4 (block forward + backward under fp16 autocast) and the SSM's
@@ -108,7 +110,7 @@ def ssm_inputs(blk, x):
         Bq = blk.B_proj(xa).view(B, T, DI, DS, 4)
         Cq = blk.C_proj(xa).view(B, T, DI, DS, 4)
         s = torch.sigmoid(blk.gate_proj(xa)) * xa
-    return delta, s, Bq, Cq
+    return delta, s, Bq, Cq, xa
 
 
 def cpu_baseline(blk, x, t_sample=256):
@@ -250,6 +252,9 @@ def box_copy_gbs(reps=20):
     return 2 * (1 << 30) / (ms * 1e-3) / 1e9
 
 
+FUSED_STAGE = "fused B/C projections + SSM (mqc_ssm_fused_bc_fwd)"
+
+
 def run_full(args):
     import torch
     from mambaqc_amd import kernels as K
@@ -277,7 +282,7 @@ def run_full(args):
     log(f"block fwd: {ms_step:.3f} ms/step, {tokens_s:.0f} tokens/s")
 
     # Fused SSM kernel alone, on the block's own operands.
-    delta, s, Bq, Cq = ssm_inputs(blk, x)
+    delta, s, Bq, Cq, xa_in = ssm_inputs(blk, x)
     la, li, Dv = (blk.Lambda_alpha.detach().float(), blk.Lambda_imag.detach().float(),
                   blk.D.detach().float())
     fn = lambda: K.ssm_forward_fused_dl(delta, s, Bq, Cq, la, li, Dv, eps=1e-6)
@@ -295,6 +300,10 @@ def run_full(args):
         stages["ssm_fused_fwd"] = ssm_ms
         stages["qln"] = event_time_ms(lambda: blk.norm(y), 10)
         stages["B_proj+C_proj GEMMs"] = event_time_ms(lambda: (blk.B_proj(s), blk.C_proj(s)), 5)
+        # The block's path at this size: B/C projections fused into the SSM kernel.
+        wbf, wcf = blk.B_proj.weight.detach(), blk.C_proj.weight.detach()
+        stages["fused B/C projections + SSM (mqc_ssm_fused_bc_fwd)"] = event_time_ms(
+            lambda: K.ssm_forward_fused_bc(xa_in, wbf, wcf, delta, s, la, li, Dv, eps=1e-6), 5)
         del y
         # A/B of the B projection alone: hipBLASLt (column blocks, the block's
         # path) against this library's MFMA GEMM (mqc_gemm_nt), same operands.
@@ -306,6 +315,14 @@ def run_full(args):
         stages["B_proj GEMM mqc_gemm_nt (MFMA, this library)"] = event_time_ms(
             lambda: mqc_gemm(xa, wb, gemm_out), 5)
         del gemm_out, xa
+        # The block's two inference paths for the B/C projections, same block and
+        # input: fused into the SSM kernel (the default at this size) and unfused
+        # (hipBLASLt GEMMs, then the SSM kernel).
+        blk.fuse_bc = True
+        stages["block forward, B/C fused into the SSM kernel"] = event_time_ms(lambda: blk(x), 5)
+        blk.fuse_bc = False
+        stages["block forward, B/C unfused (hipBLASLt + SSM)"] = event_time_ms(lambda: blk(x), 5)
+        blk.fuse_bc = None
         # The d-sliced B/C path on the same block and input (96 d's per slice:
         # 16 slices of two GEMMs and one chunked SSM each) against the whole
         # projections the block uses at this size.
@@ -314,7 +331,7 @@ def run_full(args):
         blk.bc_slice_d = None
     qln_gbs = qln_bytes(B * T, DI) / (stages["qln"] * 1e-3) / 1e9
     gemm_flop = 2 * B * T * DI * DI * DS * 4
-    del delta, s, Bq, Cq
+    del delta, s, Bq, Cq, xa_in
     torch.cuda.empty_cache()
     log(f"box calibration: 1 GiB device copy {copy_gbs:.0f} GB/s; fused SSM at "
         f"{achieved / copy_gbs:.1%} of it")
@@ -376,18 +393,21 @@ def run_full(args):
             "box_copy_GBs": round(copy_gbs, 1),
             "frac_of_box_copy": round(achieved / copy_gbs, 4),
         },
-        # The block's time is mostly the B/C projections (hipBLASLt): their
-        # MFMA roofline beside the SSM's HBM one, with this library's GEMM.
+        # Most of the block's time is the B/C projections, which at this size run
+        # fused into the SSM kernel: its MFMA roofline (both projections' flops per
+        # launch) beside the SSM's HBM one, with hipBLASLt's and this library's
+        # standalone GEMMs for one projection.
         "roofline_gemm": {
-            "kernel": "B_proj GEMM (hipBLASLt in column blocks, the block's path)",
+            "kernel": "mqc_ssm_fused_bc_fwd (B/C projections + SSM walk, the block's path)",
             "bound": "mfma",
-            "achieved": round(gemm_flop / (stages["B_proj GEMM hipBLASLt (column blocks)"] * 1e-3) / 1e12, 1),
+            "achieved": round(2 * gemm_flop / (stages[FUSED_STAGE] * 1e-3) / 1e12, 1),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(gemm_flop / (stages["B_proj GEMM hipBLASLt (column blocks)"] * 1e-3) / 1e12
-                          / PEAK_BF16_TFLOPS, 4),
-            "flop": gemm_flop,
-            "mean_launch_ms": round(stages["B_proj GEMM hipBLASLt (column blocks)"], 4),
+            "frac": round(2 * gemm_flop / (stages[FUSED_STAGE] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "flop": 2 * gemm_flop,
+            "mean_launch_ms": round(stages[FUSED_STAGE], 4),
+            "hipblaslt_B_proj_TFLOPs": round(
+                gemm_flop / (stages["B_proj GEMM hipBLASLt (column blocks)"] * 1e-3) / 1e12, 1),
             "mqc_gemm_nt_TFLOPs": round(
                 gemm_flop / (stages["B_proj GEMM mqc_gemm_nt (MFMA, this library)"] * 1e-3) / 1e12, 1),
         },

@@ -10,6 +10,8 @@ under the same seed, identical state_dict keys), and the same forward:
     delta = softplus(dt_raw); s = sigmoid(g_raw) * x_act    HIP: mqc_ssm_front_fwd
     B, C = B_proj(x_act), C_proj(x_act) as [B,T,D,S,4]      torch GEMMs (hipBLASLt)
     y = SSM(Cayley(delta * Lambda), B, s, C, D)             HIP: mqc_ssm_fused_fwd
+      (bf16 inference of whole sequences: both lines as one  HIP: mqc_ssm_fused_bc_fwd,
+       kernel that never stores B or C)
     y = QuaternionLayerNorm(y)                              HIP: mqc_qln_fwd
     y_real = out_proj(y)                                    torch GEMM
     out = x + sigmoid(z[..., :d_model]) * y_real            HIP: mqc_out_gate_fwd
@@ -36,7 +38,8 @@ import torch.nn as nn
 from . import _native as nat
 from .kernels.quaternion_norm import QuaternionLayerNorm
 from .kernels import ssm_fused as _sf
-from .kernels.ssm_fused import ssm_forward_front_dl, ssm_forward_fused_dl, ssm_front
+from .kernels.ssm_fused import (fused_bc_eligible, ssm_forward_front_dl, ssm_forward_fused_bc,
+                                ssm_forward_fused_dl, ssm_front)
 from .layers.causal_conv1d import CausalConv1d, causal_conv1d_silu, causal_conv1d_silu_step_
 from .layers.quaternion_linear import (quaternion_to_real_projection, real_to_quaternion_projection,
                                       skinny_eligible, skinny_linear)
@@ -135,6 +138,12 @@ def _rows_uniform(z: torch.Tensor) -> bool:
 # the sliced form measured 18.5-18.9 ms against 16.7 ms for the GEMMs and SSM.
 BC_WHOLE_MAX_BYTES = 32 << 30
 BC_SLICE_BYTES = 2 << 30
+
+# Inference in bf16 from this many tokens per sequence on: the B/C projections and the
+# SSM run as one kernel (mqc_ssm_fused_bc_fwd), B and C computed in 256-token tiles
+# on chip and never stored. Shorter sequences (a decode step, short prompts) would
+# fill one tile with a few tokens and keep the separate GEMMs.
+FUSED_BC_MIN_SEQ = 256
 
 
 def bc_slice_width(batch: int, seq_len: int, d_inner: int, d_state: int, elsize: int,
@@ -312,6 +321,12 @@ class QuaternionMamba2Block(nn.Module):
     int forces slices of that many d's; 0 never slices. Inference slices run
     the SSM per slice; training slices (_SlicedBCTrain) also recompute each
     slice's projections in the backward.
+
+    fuse_bc (attribute): None runs inference (no autograd) with the B/C
+    projections fused into the SSM kernel (ssm_forward_fused_bc) where that
+    kernel applies (bf16, bias-free projections, d_inner a multiple of 64, even
+    d_state <= 64) and sequences have at least FUSED_BC_MIN_SEQ tokens; True
+    also for shorter ones; False never. A forced bc_slice_d takes precedence.
     """
 
     def __init__(self, d_model: int, d_state: int = 64, d_conv: int = 4,
@@ -337,6 +352,7 @@ class QuaternionMamba2Block(nn.Module):
         self.norm = QuaternionLayerNorm(D, eps=1e-5)
         self.out_proj = quaternion_to_real_projection(D, d_model, bias=bias)
         self.bc_slice_d: int | None = None
+        self.fuse_bc: bool | None = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         xz = _linear(self.in_proj, x)
@@ -405,6 +421,11 @@ class QuaternionMamba2Block(nn.Module):
             or any(p.requires_grad for p in self.parameters()))
         width = self._bc_slice_width(x, recording)
         dt_raw, g_raw = _linear_pair(self.dt_proj, self.gate_proj, x)
+        if not recording and self._use_fused_bc(x):
+            delta, s = ssm_front(dt_raw, g_raw, x)
+            return ssm_forward_fused_bc(x, self.B_proj.weight, self.C_proj.weight, delta, s,
+                                        self.Lambda_alpha, self.Lambda_imag, self.D, eps=1e-6,
+                                        h0=h0, return_state=return_state)
         if width:
             if recording:
                 if self.B_proj.bias is not None or self.C_proj.bias is not None:
@@ -419,6 +440,19 @@ class QuaternionMamba2Block(nn.Module):
         return ssm_forward_front_dl(dt_raw, g_raw, x, Bq, Cq, self.Lambda_alpha,
                                     self.Lambda_imag, self.D, eps=1e-6, h0=h0,
                                     return_state=return_state)
+
+    def _use_fused_bc(self, x: torch.Tensor) -> bool:
+        """Whether this inference forward runs the B/C projections fused into the
+        SSM kernel (fuse_bc; the class docstring)."""
+        if self.fuse_bc is False or nat.compiling() or (self.bc_slice_d or 0) > 0:
+            return False
+        if self.B_proj.bias is not None or self.C_proj.bias is not None:
+            return False
+        if torch.is_autocast_enabled(x.device.type):
+            return False
+        if self.fuse_bc is None and x.shape[1] < FUSED_BC_MIN_SEQ:
+            return False
+        return fused_bc_eligible(x, self.B_proj.weight, self.C_proj.weight, self.d_state)
 
     def _gemm_dtype(self, x: torch.Tensor) -> torch.dtype:
         if torch.is_autocast_enabled(x.device.type):

@@ -173,8 +173,9 @@ __device__ inline void reduce_scatter32(float (&o)[64], int lane, float& r0, flo
   r1 = r2[1];
 }
 
-// FULL_T: T is a multiple of 256 (no ragged last tile).
-template <bool FULL_T>
+// FULL_T: T is a multiple of 256 (no ragged last tile). FULL_S: d_state is a multiple of
+// 32 (every half full).
+template <bool FULL_T, bool FULL_S>
 __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int tid = threadIdx.x;
@@ -237,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       // ---- 1. GEMM tile: rows [0, 128) of W_B, then [0, 128) of W_C, for the half's
       // states; states past S read state 0's rows (their results are discarded).
       const int64_t wrow0 = ((int64_t)d * S + h * kHalf) * 4;
-      const int hs = S - h * kHalf < kHalf ? S - h * kHalf : kHalf;  // states in this half
+      const int hs = FULL_S ? kHalf : (S - h * kHalf < kHalf ? S - h * kHalf : kHalf);  // states in this half
       floatx4 acc[kWB][kXB];
 #pragma unroll
       for (int i = 0; i < kWB; ++i)
@@ -289,7 +290,8 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       wait_lgkm0();
       __builtin_amdgcn_s_barrier();
 
-      // ---- 3a. Every chunk from zero: (P, H), with the chunk's q's kept for 3c.
+      // ---- 3a. Every chunk from zero: its local states hl_j and the prefix products
+      // P_j = q_j ... q_0 (kept in registers for 3c), and its transition (P_15, hl_15).
       LamConst L;
       float vv;
       {
@@ -302,10 +304,11 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
         L.a = la.x;
         L.n2 = la.y;
       }
-      float qw[kChunkLen], qc[kChunkLen];
+      quat hl[kChunkLen];
+      float pa[kChunkLen], pb[kChunkLen];
       {
         quat hh{0.f, 0.f, 0.f, 0.f};
-        float pa = 1.f, pb = 0.f;
+        float ca = 1.f, cb = 0.f;
         // Token t = cA * 16 + j: t & 31 = (cA & 1) * 16 + j, so k ^ (t & 31) = kx ^ j.
         const uint32_t tb = opaque((uint32_t)(cA * kChunkLen));
         const uint32_t kx = opaque((uint32_t)(kA ^ ((cA & 1) << 4)));
@@ -317,15 +320,16 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
           const quat Bq{bf_lo(br[0]), bf_hi(br[0]), bf_lo(br[1]), bf_hi(br[1])};
           float c;
           const quat qq = cayley_step_c(ds.x, ds.x * ds.x, L, a.eps, c);
-          qw[j] = qq.w;
-          qc[j] = c;
           hh = state_step(qq, hh, ds.y, Bq);
-          const float na = fmaf(qq.w, pa, -c * pb * vv);
-          pb = fmaf(qq.w, pb, c * pa);
-          pa = na;
+          const float na = fmaf(qq.w, ca, -c * cb * vv);
+          cb = fmaf(qq.w, cb, c * ca);
+          ca = na;
+          hl[j] = hh;
+          pa[j] = ca;
+          pb[j] = cb;
         }
         *(float4*)(lds + kOffH + (cA * kHalf + kA) * 16) = float4{hh.w, hh.x, hh.y, hh.z};
-        *(float2*)(lds + kOffP + (cA * kHalf + kA) * 8) = float2{pa, pb};
+        *(float2*)(lds + kOffP + (cA * kHalf + kA) * 8) = float2{ca, cb};
       }
       wait_lgkm0();
       __builtin_amdgcn_s_barrier();
@@ -372,23 +376,26 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       wait_lgkm0();
       __builtin_amdgcn_s_barrier();
 
-      // ---- 3c. Every chunk from its start state, with y's terms.
+      // ---- 3c. Every chunk's states from its start state h_s:
+      //   h_j = P_j (x) h_s + hl_j = pa_j h_s + pb_j (v (x) h_s) + hl_j,
+      // and y's terms C_j (x) h_j.
       {
         const float4 e = *(const float4*)(lds + kOffH + (cA * kHalf + kA) * 16);
-        quat hh{e.x, e.y, e.z, e.w};
+        const quat hs0{e.x, e.y, e.z, e.w};
+        const quat vh = qmul(quat{0.f, L.v0, L.v1, L.v2}, hs0);
         float o[4 * kChunkLen];
-        const bool live = kA < hs;
+        const bool live = FULL_S || kA < hs;
         const uint32_t tb = opaque((uint32_t)(cA * kChunkLen));
         const uint32_t kx = opaque((uint32_t)(kA ^ ((cA & 1) << 4)));
 #pragma unroll
         for (int j = 0; j < kChunkLen; ++j) {
           const uint32_t t = tb + j;
-          const float2 ds = *(const float2*)(lds + kOffDS + t * 8);
-          const u32x4 r = *(const u32x4*)(lds + t * kTokBytes + ((kx ^ j) << 4));
-          const quat Bq{bf_lo(r[0]), bf_hi(r[0]), bf_lo(r[1]), bf_hi(r[1])};
-          const quat Cq{bf_lo(r[2]), bf_hi(r[2]), bf_lo(r[3]), bf_hi(r[3])};
-          const quat qq{qw[j], qc[j] * L.v0, qc[j] * L.v1, qc[j] * L.v2};
-          hh = state_step(qq, hh, ds.y, Bq);
+          const u32x2 r = *(const u32x2*)(lds + t * kTokBytes + ((kx ^ j) << 4) + 8);
+          const quat Cq{bf_lo(r[0]), bf_hi(r[0]), bf_lo(r[1]), bf_hi(r[1])};
+          const quat hh{fmaf(pa[j], hs0.w, fmaf(pb[j], vh.w, hl[j].w)),
+                        fmaf(pa[j], hs0.x, fmaf(pb[j], vh.x, hl[j].x)),
+                        fmaf(pa[j], hs0.y, fmaf(pb[j], vh.y, hl[j].y)),
+                        fmaf(pa[j], hs0.z, fmaf(pb[j], vh.z, hl[j].z))};
           const quat oc = qmul(Cq, hh);
           o[4 * j + 0] = live ? oc.w : 0.f;
           o[4 * j + 1] = live ? oc.x : 0.f;
@@ -476,8 +483,10 @@ int mqc_ssm_fused_bc_fwd(const void* x, const void* B_weight, const void* C_weig
   if (e != hipSuccess) return (int)e;
   if (dev < 0 || dev >= kMaxDevices) return MQC_E_LIMIT;
   if (!g_fused_attr_set[dev].load(std::memory_order_acquire)) {
-    int st = set_lds_limit(fused_bc_ssm_kernel<true>);
-    if (st == MQC_OK) st = set_lds_limit(fused_bc_ssm_kernel<false>);
+    int st = set_lds_limit(fused_bc_ssm_kernel<true, true>);
+    if (st == MQC_OK) st = set_lds_limit(fused_bc_ssm_kernel<true, false>);
+    if (st == MQC_OK) st = set_lds_limit(fused_bc_ssm_kernel<false, true>);
+    if (st == MQC_OK) st = set_lds_limit(fused_bc_ssm_kernel<false, false>);
     if (st != MQC_OK) return st;
     g_fused_attr_set[dev].store(true, std::memory_order_release);
   }
@@ -489,10 +498,15 @@ int mqc_ssm_fused_bc_fwd(const void* x, const void* B_weight, const void* C_weig
   a.batch = (int)batch; a.T = (int)seq_len; a.Dm = (int)d_inner; a.S = (int)d_state; a.eps = eps;
   const dim3 grid((unsigned)(batch * d_inner));
   hipStream_t st = (hipStream_t)stream;
-  if (seq_len % kT == 0)
-    hipLaunchKernelGGL(fused_bc_ssm_kernel<true>, grid, dim3(kThreads), kLdsFused, st, a);
+  const bool full_t = seq_len % kT == 0, full_s = d_state % kHalf == 0;
+  if (full_t && full_s)
+    hipLaunchKernelGGL((fused_bc_ssm_kernel<true, true>), grid, dim3(kThreads), kLdsFused, st, a);
+  else if (full_t)
+    hipLaunchKernelGGL((fused_bc_ssm_kernel<true, false>), grid, dim3(kThreads), kLdsFused, st, a);
+  else if (full_s)
+    hipLaunchKernelGGL((fused_bc_ssm_kernel<false, true>), grid, dim3(kThreads), kLdsFused, st, a);
   else
-    hipLaunchKernelGGL(fused_bc_ssm_kernel<false>, grid, dim3(kThreads), kLdsFused, st, a);
+    hipLaunchKernelGGL((fused_bc_ssm_kernel<false, false>), grid, dim3(kThreads), kLdsFused, st, a);
   return launch_status();
 }
 

@@ -156,3 +156,31 @@ def test_fused_bc_rejects_what_it_cannot_run():
         K.ssm_forward_fused_bc(x.float(), wb.float(), wc.float(), delta, s, la, li, D)
     with pytest.raises(RuntimeError):
         K.ssm_forward_fused_bc(x, wb.requires_grad_(), wc, delta, s, la, li, D)
+
+
+def test_block_forward_fused_bc_path():
+    """QuaternionMamba2Block inference in bf16 takes the fused path from
+    FUSED_BC_MIN_SEQ tokens on: its output against the same block with fusion off
+    and against the CPU oracle of the block (fp32 on the same bf16 weights), and a
+    sequence fed in two pieces through forward_with_state against the whole."""
+    import mambaqc_amd
+    from mambaqc_amd import block as blockmod
+
+    torch.manual_seed(0)
+    blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=16).to(DEV, BF).eval()
+    g = torch.Generator(device=DEV).manual_seed(1)
+    x = torch.randn(2, 300, 64, generator=g, device=DEV).to(BF)
+    assert x.shape[1] >= blockmod.FUSED_BC_MIN_SEQ and blk._use_fused_bc(
+        torch.empty(2, 300, blk.d_inner, device=DEV, dtype=BF))
+    with torch.no_grad():
+        got = blk(x)
+        blk.fuse_bc = False
+        ref_unfused = blk(x)
+        blk.fuse_bc = None
+        out1, st = blk.forward_with_state(x[:, :260])
+        out2, _ = blk.forward_with_state(x[:, 260:], st)
+    assert_close(got, ref_unfused, 2e-2, "block fused vs unfused")
+    sd = {k: v.detach().float().cpu() for k, v in blk.state_dict().items()}
+    want = oracle.block_forward_reference(sd, x.float().cpu(), d_state=16)
+    assert_close(got, want, 2e-2, "block fused vs oracle")
+    assert_close(torch.cat([out1, out2], 1), got, 2e-2, "fused block in pieces vs whole")
