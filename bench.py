@@ -1,7 +1,7 @@
 """Benchmark: QuaternionMamba2Block forward on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
-                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_train|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|fused_bc|bc_unfused|decode|decode_graph|block_long|train|copy]
+                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_train|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|fused_bc|bc_unfused|out_step|out_step_unfused|decode|decode_graph|block_long|train|copy]
                     [--preset small|base|large]
 
 Workload (BASELINE configs[2]/[3] shape): one QuaternionMamba2Block forward,
@@ -318,11 +318,15 @@ def run_full(args):
         # The block's two inference paths for the B/C projections, same block and
         # input: fused into the SSM kernel (the default at this size) and unfused
         # (hipBLASLt GEMMs, then the SSM kernel).
-        blk.fuse_bc = True
-        stages["block forward, B/C fused into the SSM kernel"] = event_time_ms(lambda: blk(x), 5)
+        stages["block forward (default: B/C fused into the SSM, fused output step)"] = \
+            event_time_ms(lambda: blk(x), 5)
         blk.fuse_bc = False
         stages["block forward, B/C unfused (hipBLASLt + SSM)"] = event_time_ms(lambda: blk(x), 5)
         blk.fuse_bc = None
+        blk.fuse_out = False
+        stages["block forward, output step unfused (out_proj + gate kernel)"] = \
+            event_time_ms(lambda: blk(x), 5)
+        blk.fuse_out = None
         # The d-sliced B/C path on the same block and input (96 d's per slice:
         # 16 slices of two GEMMs and one chunked SSM each) against the whole
         # projections the block uses at this size.
@@ -756,6 +760,22 @@ def run_kernel_loop(args):
                     Bq = wide_linear(x, wb).view(B, T, DI, DS, 4)
                     Cq = wide_linear(x, wc).view(B, T, DI, DS, 4)
                     return K.ssm_forward_fused_dl(delta, s, Bq, Cq, la, li, Dv)
+            nbytes = 0
+        elif args.mode in ("out_step", "out_step_unfused"):
+            # Config 3's output step: out_proj ([8192, 6144] x [6144, 768]) with the gate
+            # and residual, as one kernel (mqc_out_proj_gate_fwd) or unfused (F.linear,
+            # then mqc_out_gate_fwd), on the same operands.
+            from mambaqc_amd.block import out_gate, out_proj_gate
+            bf = torch.bfloat16
+            xo = torch.randn(B * T, DM, generator=g, device="cuda").to(bf)
+            xz = torch.randn(B * T, 2 * DI, generator=g, device="cuda").to(bf)
+            zo = xz[:, DI:]
+            yo = torch.randn(B * T, DI, 4, generator=g, device="cuda").to(bf)
+            wo = (torch.randn(DM, 4 * DI, generator=g, device="cuda") * 0.02).to(bf)
+            if args.mode == "out_step":
+                fn = lambda: out_proj_gate(xo, zo, yo, wo)
+            else:
+                fn = lambda: out_gate(xo, zo, torch.nn.functional.linear(yo.view(B * T, -1), wo))
             nbytes = 0
         elif args.mode == "copy":
             src = torch.empty(1 << 28, device="cuda")  # 1 GiB

@@ -212,6 +212,22 @@ int mqc_ssm_fused_bc_fwd(const void* x, const void* B_weight, const void* C_weig
                          void* h_last, int64_t batch, int64_t seq_len, int64_t d_inner,
                          int64_t d_state, float eps, int dtype, void* stream);
 
+/* The block's output step in one launch, bf16 only (dtype MQC_BF16):
+ *   out[r, n] = x[r, n] + sigmoid(z[r, n]) * bf16(sum_j y[r, j] W[n, j] + bias[n])
+ * for r < rows, n < d_model: the quaternion -> real projection out_proj of the
+ * QuaternionLayerNorm output y [rows, k] (k = 4 * d_inner, components innermost) by
+ * W [d_model, k] (+ bias [d_model] or NULL), rounded to bf16 as the projection stores
+ * it, gated by z [rows, >= d_model] (row stride z_row_stride elements, read in place:
+ * the gate half of in_proj's output) and added to the residual x [rows, d_model].
+ * y, W, x, z, out 16-byte aligned; d_model a multiple of 8, k of 64, z_row_stride of 8.
+ * Replaces out_proj (QuaternionLinear._forward_quaternion_to_real,
+ * mambaqc/layers/quaternion_linear.py:163-172) with the gate and residual of
+ * mambaqc/models/quaternion_mamba2_block.py:157-164 (z[..., :d_model], as the
+ * reference's Lite block gates), which mqc_out_gate_fwd covers unfused. */
+int mqc_out_proj_gate_fwd(const void* y, const void* W, const void* bias, const void* x,
+                          const void* z, int64_t z_row_stride, void* out, int64_t rows,
+                          int64_t d_model, int64_t k, int dtype, void* stream);
+
 /* C[M, N] = X[M, K] . W[N, K]^T in bf16 with fp32 accumulation (dtype must be
  * MQC_BF16), contiguous row-major X, W, C, 16-byte aligned; N a multiple of
  * 256, K of 64, M any. The hand-written MFMA GEMM of the block's B/C

@@ -71,6 +71,7 @@ SIGNATURES = {
     "mqc_ssm_noalloc_prepare": [],
     "mqc_ssm_fused_bc_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                              _i64, _i64, _i64, _i64, _f32, _int, _vp],
+    "mqc_out_proj_gate_fwd": [_vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _int, _vp],
 }
 
 # name -> argtypes of the entry points that return int64_t (a size, or a

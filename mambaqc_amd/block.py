@@ -15,6 +15,7 @@ under the same seed, identical state_dict keys), and the same forward:
     y = QuaternionLayerNorm(y)                              HIP: mqc_qln_fwd
     y_real = out_proj(y)                                    torch GEMM
     out = x + sigmoid(z[..., :d_model]) * y_real            HIP: mqc_out_gate_fwd
+      (bf16 inference: both lines as one kernel,             HIP: mqc_out_proj_gate_fwd)
 
 z, q and the quaternion S are never materialised: the SSM kernel discretises
 in registers and takes the real selected signal s. When autograd is recording,
@@ -117,6 +118,56 @@ def out_gate(x: torch.Tensor, z: torch.Tensor, y_real: torch.Tensor) -> torch.Te
     return out
 
 
+def out_proj_gate_eligible(x: torch.Tensor, z: torch.Tensor, y: torch.Tensor,
+                           weight: torch.Tensor, bias: torch.Tensor | None) -> bool:
+    """Whether out_proj_gate takes these operands: bf16 on a ROCm device, x
+    [..., d_model] with d_model a multiple of 8, y [..., n, 4] with 4 n a multiple
+    of 64, weight [d_model, 4 n], z's gate half readable as rows 16-byte aligned."""
+    if not (x.is_cuda and z.is_cuda and y.is_cuda and weight.is_cuda):
+        return False
+    tensors = (x, z, y, weight) + (() if bias is None else (bias,))
+    if any(t.dtype != torch.bfloat16 for t in tensors):
+        return False
+    d = x.shape[-1]
+    k = y.shape[-2] * 4 if y.dim() >= 2 else 0
+    if d % 8 or k % 64 or k == 0 or tuple(weight.shape) != (d, k):
+        return False
+    if z.shape[:-1] != x.shape[:-1] or z.shape[-1] < d or z.stride(-1) != 1:
+        return False
+    zs = z.stride(-2) if z.dim() > 1 else z.shape[-1]
+    return (z.dim() == 1 or _rows_uniform(z)) and zs % 8 == 0 and z.data_ptr() % 16 == 0
+
+
+def out_proj_gate(x: torch.Tensor, z: torch.Tensor, y: torch.Tensor, weight: torch.Tensor,
+                  bias: torch.Tensor | None = None) -> torch.Tensor:
+    """The block's output step in one HIP launch (inference, bf16):
+    x + sigmoid(z[..., :d_model]) * out_proj(y), out_proj the quaternion -> real
+    projection of y [..., n, 4] by weight [d_model, 4 n] (+ bias), its result rounded
+    to bf16 as the projection stores it and gated without leaving the chip
+    (mambaqc/layers/quaternion_linear.py:163-172 and
+    mambaqc/models/quaternion_mamba2_block.py:157-164). z may be the strided gate
+    half of in_proj's output; it is read in place."""
+    nat.require_device("out_proj_gate", x, z, y, weight)
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                       for t in (x, z, y, weight, bias)):
+        raise RuntimeError("out_proj_gate: inference only; run under torch.no_grad")
+    if not out_proj_gate_eligible(x, z, y, weight, bias):
+        raise ValueError("out_proj_gate: needs bf16 operands, d_model a multiple of 8, 4 n a "
+                         "multiple of 64 and z rows 16-byte aligned")
+    d = x.shape[-1]
+    xc = nat.aligned16(x.detach())
+    yc = nat.aligned16(y.detach())
+    wc = nat.aligned16(weight.detach())
+    bc = None if bias is None else bias.detach().contiguous()
+    rows = xc.numel() // d
+    zs = z.stride(-2) if z.dim() > 1 else z.shape[-1]
+    out = torch.empty_like(xc)
+    nat.call("mqc_out_proj_gate_fwd", xc, yc.data_ptr(), wc.data_ptr(), nat.ptr(bc),
+             xc.data_ptr(), z.data_ptr(), zs, out.data_ptr(), rows, d, weight.shape[1],
+             nat.BF16, nat.stream_of(xc))
+    return out
+
+
 def _rows_uniform(z: torch.Tensor) -> bool:
     """True when all leading axes of z collapse to a single row stride."""
     expected = z.stride(-2)
@@ -144,6 +195,10 @@ BC_SLICE_BYTES = 2 << 30
 # on chip and never stored. Shorter sequences (a decode step, short prompts) would
 # fill one tile with a few tokens and keep the separate GEMMs.
 FUSED_BC_MIN_SEQ = 256
+# bf16 inference with at least this many token rows runs the output step (out_proj +
+# gate + residual) as one kernel (mqc_out_proj_gate_fwd); decode-sized steps keep the
+# skinny GEMM and the gate kernel.
+FUSED_OUT_MIN_ROWS = 1024
 
 
 def bc_slice_width(batch: int, seq_len: int, d_inner: int, d_state: int, elsize: int,
@@ -327,6 +382,10 @@ class QuaternionMamba2Block(nn.Module):
     kernel applies (bf16, bias-free projections, d_inner a multiple of 64, even
     d_state <= 64) and sequences have at least FUSED_BC_MIN_SEQ tokens; True
     also for shorter ones; False never. A forced bc_slice_d takes precedence.
+
+    fuse_out (attribute): None runs the output step of bf16 inference (out_proj,
+    gate, residual) as one kernel (out_proj_gate) from FUSED_OUT_MIN_ROWS token
+    rows on; True for any number of rows; False never.
     """
 
     def __init__(self, d_model: int, d_state: int = 64, d_conv: int = 4,
@@ -353,6 +412,7 @@ class QuaternionMamba2Block(nn.Module):
         self.out_proj = quaternion_to_real_projection(D, d_model, bias=bias)
         self.bc_slice_d: int | None = None
         self.fuse_bc: bool | None = None
+        self.fuse_out: bool | None = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         xz = _linear(self.in_proj, x)
@@ -361,8 +421,19 @@ class QuaternionMamba2Block(nn.Module):
         x_act = causal_conv1d_silu(x_in, conv.weight, conv.bias)
         y = self._ssm_forward(x_act)
         y = self.norm(y)
-        y_real = _out_proj(self.out_proj, y)
-        return out_gate(x, z, y_real)
+        return self._output_step(x, z, y)
+
+    def _output_step(self, x: torch.Tensor, z: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+        """x + sigmoid(z[..., :d_model]) * out_proj(y): one fused launch for bf16
+        inference where it applies (fuse_out), else out_proj then out_gate."""
+        op = self.out_proj
+        if (self.fuse_out is not False and not nat.compiling()
+                and not (torch.is_grad_enabled() and (y.requires_grad or x.requires_grad
+                                                      or op.weight.requires_grad))
+                and (self.fuse_out or x.numel() // max(x.shape[-1], 1) >= FUSED_OUT_MIN_ROWS)
+                and out_proj_gate_eligible(x, z, y, op.weight, op.bias)):
+            return out_proj_gate(x, z, y, op.weight, op.bias)
+        return out_gate(x, z, _out_proj(op, y))
 
     def forward_with_state(self, x: torch.Tensor, state=None):
         """forward() continued from a recurrent state; returns (out, new_state).

@@ -244,7 +244,8 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       for (int i = 0; i < kWB; ++i)
 #pragma unroll
         for (int j = 0; j < kXB; ++j) acc[i][j] = (floatx4){};
-      auto wrow = [&](int g, int k0) -> const void* {
+      auto wrow = [&](int g, int k0, int i, uint32_t& voff, const DmaLane& dl) -> const void* {
+        voff = (uint32_t)(dl.lrow * K * 2) + dl.cb(i);
         const int r = g & 127;  // 8-row groups never straddle B and C
         const int rr = r < hs * 4 ? r : 0;
         const __bf16* base = g < 128 ? a.wb : a.wc;
@@ -252,19 +253,19 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       };
       auto xrow = [&](int g, int k0, int i, uint32_t& voff, const DmaLane& dl) -> const void* {
         if (FULL_T || tv == kT) {
-          voff = (uint32_t)(dl.lrow * K * 2) + dl.cbyte[i & 1];
+          voff = (uint32_t)(dl.lrow * K * 2) + dl.cb(i);
           return a.x + ((xrow0 + g) * K + k0);
         }
         // The ragged last tile: tokens past the sequence read its last token.
         const int gb = g < tv ? g : tv - 1;
         const int r = g + dl.lrow < tv ? g + dl.lrow : tv - 1;
-        voff = (uint32_t)((r - gb) * K * 2) + dl.cbyte[i & 1];
+        voff = (uint32_t)((r - gb) * K * 2) + dl.cb(i);
         return a.x + ((xrow0 + gb) * K + k0);
       };
       // In a ragged last half (d_state not a multiple of 32) the 8-row groups of a DMA
       // instruction are two whole states (d_state is even), so clamping the group's
       // base row keeps every lane's row inside the half.
-      tile_kloop(K, K, lds, acc, wrow, xrow);
+      tile_kloop(K, lds, acc, wrow, xrow);
       if (h == 0 && tid < kT) *(float2*)(lds + kOffDS + tid * 8) = float2{dl_t, s_t};
 
       // ---- 2. The tile, rounded to bf16, over the stages (every wave is past its last

@@ -50,20 +50,23 @@ __device__ inline void gemm_tile(const __bf16* __restrict__ X, const __bf16* __r
   for (int a = 0; a < kWB; ++a)
 #pragma unroll
     for (int b = 0; b < kXB; ++b) acc[a][b] = (floatx4){};
-  auto wrow = [&](int g, int k0) -> const void* { return W + ((int64_t)(n0 + g) * K + k0); };
+  auto wrow = [&](int g, int k0, int i, uint32_t& voff, const DmaLane& dl) -> const void* {
+    voff = (uint32_t)(dl.lrow * K * 2) + dl.cb(i);
+    return W + ((int64_t)(n0 + g) * K + k0);
+  };
   auto xrow = [&](int g, int k0, int i, uint32_t& voff, const DmaLane& dl) -> const void* {
     if constexpr (FULL_M) {
-      voff = (uint32_t)(dl.lrow * K * 2) + dl.cbyte[i & 1];
+      voff = (uint32_t)(dl.lrow * K * 2) + dl.cb(i);
       return X + ((int64_t)(m0 + g) * K + k0);
     } else {
       // The last row tile: rows past M read row M - 1.
       const int gb = m0 + g < M ? m0 + g : M - 1;
       const int r = m0 + g + dl.lrow < M ? m0 + g + dl.lrow : M - 1;
-      voff = (uint32_t)((r - gb) * K * 2) + dl.cbyte[i & 1];
+      voff = (uint32_t)((r - gb) * K * 2) + dl.cb(i);
       return X + ((int64_t)gb * K + k0);
     }
   };
-  tile_kloop(K, K, lds, acc, wrow, xrow);
+  tile_kloop(K, lds, acc, wrow, xrow);
 
   // Epilogue through LDS (every wave is past its last LDS read at the barrier).
   wait_lgkm0();

@@ -1,7 +1,8 @@
 #pragma once
 // The MFMA main loop shared by the library's bf16 GEMM tiles (gfx950):
-//   acc += W_tile[256 rows, K] . X_tile[256 rows, K]^T
-// for one 256 x 256 output tile, fp32 accumulation.
+//   acc += W_tile[TW rows, K] . X_tile[TX rows, K]^T
+// for one output tile, fp32 accumulation. Described here for the 256 x 256 tile of the
+// projections (Tile256); TileCfg gives smaller tiles the same loop.
 //
 //   - 8 waves (two per SIMD); wave w owns W rows (w >> 2) * 128 + [0, 128) and X rows
 //     (w & 3) * 64 + [0, 64) as 8 x 4 blocks of v_mfma_f32_16x16x32_bf16 accumulators
@@ -87,44 +88,79 @@ struct DmaLane {
 #pragma unroll
     for (int p = 0; p < 2; ++p) cbyte[p] = (uint32_t)((lslot ^ ((p * 4 + (lrow >> 1)) & 7)) * 16);
   }
+  // The chunk offset of DMA group i (selected: i may be a wave-dependent value, and an
+  // indexed register array would go to scratch).
+  __device__ uint32_t cb(int i) const { return (i & 1) ? cbyte[1] : cbyte[0]; }
 };
 
+// Tile shape: TW rows of W by TX rows of X, NW_W x NW_X waves (wave w owns W rows
+// (w / NW_X) * (TW / NW_W) + [0, TW / NW_W) and X rows (w % NW_X) * (TX / NW_X) + [0, TX / NW_X)
+// as WB x XB blocks of 16 x 16 accumulators). Every DMA instruction carries 8 rows of one
+// operand; a wave issues TW / 8 / waves of them for W and TX / 8 / waves for X per stage.
+template <int TW_, int TX_, int NW_W_, int NW_X_>
+struct TileCfg {
+  static constexpr int TW = TW_, TX = TX_, NW_W = NW_W_, NW_X = NW_X_;
+  static constexpr int kWaves = NW_W * NW_X;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int WB = TW / NW_W / 16;
+  static constexpr int XB = TX / NW_X / 16;
+  static constexpr int kWBytes = TW * kRowBytes;              // W tile of one stage
+  static constexpr int kStageBytes = (TW + TX) * kRowBytes;
+  static constexpr int kStagesBytes = 2 * kStageBytes;
+  static constexpr int kWLoads = TW / kRowsPerLoad / kWaves;  // DMA instructions per wave
+  static constexpr int kXLoads = TX / kRowsPerLoad / kWaves;
+  static_assert(TW % (16 * NW_W) == 0 && TX % (16 * NW_X) == 0, "whole 16-row blocks");
+  static_assert(TW % (kRowsPerLoad * kWaves) == 0 && TX % (kRowsPerLoad * kWaves) == 0,
+                "whole DMA groups per wave");
+};
+
+// The library's 256 x 256 tile (8 waves of 128 W rows x 64 X rows).
+using Tile256 = TileCfg<kT, kT, 2, 4>;
+static_assert(Tile256::WB == kWB && Tile256::XB == kXB && Tile256::kStagesBytes == kStagesBytes,
+              "the 256 x 256 constants above");
+
 // The K loop of one tile into acc (which it does not clear). For DMA instruction i of
-// this wave (tile rows g .. g + 7, g = (wave * kLoads + i) * 8) and K offset k0 (in
-// elements):
-//   wrow(g, k0)           -> wave-uniform pointer to W's row g, column k0; the lane reads
-//                            row g + lrow at byte offset lrow * ld_w * 2 + cbyte;
-//   xrow(g, k0, i, voff)  -> wave-uniform pointer for X's rows, with the lane's byte
-//                            offset from it written to voff (the caller may clamp rows).
+// this wave (tile rows g .. g + 7 of one operand) and K offset k0 (in elements):
+//   wrow(g, k0, i, voff, dl), xrow(g, k0, i, voff, dl)
+//       -> a wave-uniform pointer for W's (X's) rows g .. g + 7 at column k0, with the
+//          lane's byte offset from it written to voff: lane row dl.lrow, 16-byte chunk
+//          dl.cb(i) (i the operand's DMA group index, whose parity sets the
+//          swizzle), row pitch ld * 2 bytes; the caller may clamp rows past the matrix.
 // Returns after the last MFMA; the caller waits on lgkmcnt and barriers before reusing
 // the LDS stages.
-template <typename WRow, typename XRow>
-__device__ inline void tile_kloop(int K, int ld_w, char* lds, floatx4 (&acc)[kWB][kXB],
-                                  const WRow& wrow, const XRow& xrow) {
+template <typename Cfg, typename WRow, typename XRow>
+__device__ inline void tile_kloop_cfg(int K, char* lds,
+                                      floatx4 (&acc)[Cfg::WB][Cfg::XB], const WRow& wrow,
+                                      const XRow& xrow) {
+  constexpr int WB = Cfg::WB, XB = Cfg::XB;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const DmaLane dl(lane);
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)lds;
-  uint32_t wvoff[2];
-#pragma unroll
-  for (int p = 0; p < 2; ++p) wvoff[p] = (uint32_t)(dl.lrow * ld_w * 2) + dl.cbyte[p];
   auto issue_stage = [&](int kt) {
     const int k0 = kt * kBK;
-    const uint32_t sb = lds0 + (uint32_t)((kt & 1) * kStageBytes);
+    const uint32_t sb = lds0 + (uint32_t)((kt & 1) * Cfg::kStageBytes);
+    constexpr int NL = Cfg::kWLoads > Cfg::kXLoads ? Cfg::kWLoads : Cfg::kXLoads;
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int g = (wave * kLoads + i) * kRowsPerLoad;
-      const uint32_t off = (uint32_t)((wave * kLoads + i) * 1024);
-      dma16(wrow(g, k0), wvoff[i & 1], sb + off);
-      uint32_t xv;
-      const void* xb = xrow(g, k0, i, xv, dl);
-      dma16(xb, xv, sb + kTileBytes + off);
+    for (int i = 0; i < NL; ++i) {
+      if (i < Cfg::kWLoads) {
+        const int gi = wave * Cfg::kWLoads + i;
+        uint32_t wv;
+        const void* wb = wrow(gi * kRowsPerLoad, k0, gi, wv, dl);
+        dma16(wb, wv, sb + (uint32_t)(gi * 1024));
+      }
+      if (i < Cfg::kXLoads) {
+        const int gi = wave * Cfg::kXLoads + i;
+        uint32_t xv;
+        const void* xb = xrow(gi * kRowsPerLoad, k0, gi, xv, dl);
+        dma16(xb, xv, sb + (uint32_t)(Cfg::kWBytes + gi * 1024));
+      }
     }
   };
 
-  const int wn = wave >> 2;
-  const int wm = wave & 3;
+  const int wn = wave / Cfg::NW_X;
+  const int wm = wave % Cfg::NW_X;
   const int rl = lane & 15;  // row within a 16-row block
   const int q = lane >> 4;   // 16-byte chunk within a 32-wide K slice
   // LDS byte offsets of this lane's fragments per K slice; the blocks of a wave are
@@ -133,23 +169,23 @@ __device__ inline void tile_kloop(int K, int ld_w, char* lds, floatx4 (&acc)[kWB
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
     const int c = 4 * kk + q;
-    const int rw = wn * 128 + rl;
+    const int rw = wn * (Cfg::TW / Cfg::NW_W) + rl;
     woff[kk] = rw * kRowBytes + gswz(rw, c) * 16;
-    const int rx = wm * 64 + rl;
-    xoff[kk] = kTileBytes + rx * kRowBytes + gswz(rx, c) * 16;
+    const int rx = wm * (Cfg::TX / Cfg::NW_X) + rl;
+    xoff[kk] = Cfg::kWBytes + rx * kRowBytes + gswz(rx, c) * 16;
   }
-  bf16x8 wf[2][kWB], xf[2][kXB];
+  bf16x8 wf[2][WB], xf[2][XB];
   auto read_frags = [&](int buf, const char* sb, int kk) {
 #pragma unroll
-    for (int nb = 0; nb < kWB; ++nb) wf[buf][nb] = *(const bf16x8*)(sb + woff[kk] + nb * 16 * kRowBytes);
+    for (int nb = 0; nb < WB; ++nb) wf[buf][nb] = *(const bf16x8*)(sb + woff[kk] + nb * 16 * kRowBytes);
 #pragma unroll
-    for (int mb = 0; mb < kXB; ++mb) xf[buf][mb] = *(const bf16x8*)(sb + xoff[kk] + mb * 16 * kRowBytes);
+    for (int mb = 0; mb < XB; ++mb) xf[buf][mb] = *(const bf16x8*)(sb + xoff[kk] + mb * 16 * kRowBytes);
   };
   auto mfmas = [&](int buf) {
 #pragma unroll
-    for (int nb = 0; nb < kWB; ++nb)
+    for (int nb = 0; nb < WB; ++nb)
 #pragma unroll
-      for (int mb = 0; mb < kXB; ++mb)
+      for (int mb = 0; mb < XB; ++mb)
         acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[buf][nb], xf[buf][mb], acc[nb][mb], 0, 0, 0);
   };
 
@@ -160,14 +196,14 @@ __device__ inline void tile_kloop(int K, int ld_w, char* lds, floatx4 (&acc)[kWB
     wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
     if (kt + 1 < KT) issue_stage(kt + 1);
-    const char* sbase = lds + (kt & 1) * kStageBytes;
+    const char* sbase = lds + (kt & 1) * Cfg::kStageBytes;
     read_frags(0, sbase, 0);
     __builtin_amdgcn_sched_barrier(0);
     // First K slice: its MFMAs with the second slice's fragment reads, one after each MFMA.
     read_frags(1, sbase, 1);
     mfmas(0);
 #pragma unroll
-    for (int g = 0; g < kWB + kXB; ++g) {
+    for (int g = 0; g < WB + XB; ++g) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
     }
@@ -175,6 +211,13 @@ __device__ inline void tile_kloop(int K, int ld_w, char* lds, floatx4 (&acc)[kWB
     mfmas(1);
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// The 256 x 256 tile's K loop.
+template <typename WRow, typename XRow>
+__device__ inline void tile_kloop(int K, char* lds, floatx4 (&acc)[kWB][kXB], const WRow& wrow,
+                                  const XRow& xrow) {
+  tile_kloop_cfg<Tile256>(K, lds, acc, wrow, xrow);
 }
 
 }  // namespace mfma

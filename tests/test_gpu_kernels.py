@@ -468,10 +468,11 @@ def test_block_bf16_vs_oracle():
 def test_block_headline_width_bf16_vs_oracle():
     """The headline configuration's block (d_model 768, d_state 64, expand 2:
     d_inner 1536) in bf16 at B4 T256 against the oracle in fp32 on the same
-    bf16-rounded weights and input. 1024 token rows make the B/C projections
-    take wide_linear's column blocks (1.2 GB of weight each), and the SSM takes
-    the inference walk with four states per lane (384-thread blocks): the
-    composition the benchmark times."""
+    bf16-rounded weights and input, on both of its inference paths: the default
+    (256 tokens per sequence and 1024 token rows: the B/C projections fused into
+    the SSM kernel, and the output step as one kernel, as the benchmark times) and
+    the unfused one (wide_linear's column blocks of 1.2 GB of weight each, the
+    inference walk with four states per lane, out_proj then the gate kernel)."""
     from mambaqc_amd.layers import quaternion_linear as ql
 
     torch.manual_seed(11)
@@ -482,12 +483,17 @@ def test_block_headline_width_bf16_vs_oracle():
                     device=DEV).to(torch.bfloat16)
     n, k = blk.B_proj.weight.shape
     assert len(ql._blocks(n, k, 2)) > 1 and x.numel() // 768 >= ql.WIDE_LINEAR_MIN_ROWS
+    x_act = torch.empty(4, 256, blk.d_inner, device=DEV, dtype=torch.bfloat16)
+    assert blk._use_fused_bc(x_act)
     with torch.no_grad():
         got = blk(x)
+        blk.fuse_bc = blk.fuse_out = False
+        got_unfused = blk(x)
     assert got.dtype == torch.bfloat16
     sd = {kk: v.detach().float().cpu() for kk, v in blk.state_dict().items()}
     want = oracle.block_forward_reference(sd, x.float().cpu(), d_state=64)
-    assert_close(got, want, 2e-2, "block d768 s64 e2 bf16")
+    assert_close(got, want, 2e-2, "block d768 s64 e2 bf16 (fused paths)")
+    assert_close(got_unfused, want, 2e-2, "block d768 s64 e2 bf16 (unfused)")
 
 
 def test_block_built_under_inference_mode():
