@@ -47,8 +47,9 @@ constexpr int kHalf = 32;                 // states per half
 constexpr int kMaxHalves = 2;             // d_state <= 64
 constexpr int kNChunk = 16;               // chunks per tile
 constexpr int kChunkLen = kT / kNChunk;   // 16 tokens
-constexpr int kCellBytes = 16;            // bf16 B and C quaternions of one (token, state)
-constexpr int kTokBytes = kHalf * kCellBytes;  // 512 bytes per token in the B/C tile
+constexpr int kCellBytes = 8;             // one bf16 quaternion of one (token, state)
+constexpr int kTokBytes = kHalf * kCellBytes;  // 256 bytes per token in the B or the C tile
+constexpr int kOffC = kT * kTokBytes;          // the C tile after the B tile (64 KiB each)
 // LDS layout (bytes): the GEMM's two stages, reused for the B/C tile, then the walk's own.
 constexpr int kOffH = kStagesBytes;                          // chunk states [16][32] quat
 constexpr int kOffP = kOffH + kNChunk * kHalf * 16;          // chunk products [16][32] float2
@@ -58,7 +59,10 @@ constexpr int kOffHC = kOffDS + kT * 8;                      // carried states [
 constexpr int kOffLT = kOffHC + kMaxHalves * kHalf * 16;     // Cayley constants [64] 2 x float4
 constexpr int kLdsFused = kOffLT + kMaxHalves * kHalf * 32;  // 149 KiB
 
-static_assert(kT * kTokBytes == kStagesBytes, "the B/C tile fills the GEMM's stages");
+// The B tile is LDS stage 0 and the C tile stage 1: the walk's first pass reads only B,
+// the second only C.
+static_assert(2 * kT * kTokBytes == kStagesBytes && kOffC == kStageBytes,
+              "the B and C tiles are the GEMM's two stages");
 static_assert(kLdsFused <= 160 * 1024, "gfx950 LDS");
 
 struct FusedArgs {
@@ -77,9 +81,45 @@ struct FusedArgs {
   float eps;
 };
 
-// The B/C tile: token t's 32 cells (state k at cell k ^ (t & 31)) form one 512-byte row,
-// so the 16 tokens one epilogue store instruction writes spread over the banks, while
-// the 32 states one walk read takes stay one contiguous row.
+// The B and C tiles: token t's 32 quaternions (state k at cell k ^ (t & 15)) form one
+// 256-byte row, so the 16 tokens one epilogue store instruction writes spread over the
+// banks, while the 32 states one walk read takes stay one contiguous row.
+
+// Rows of one K stage for the GEMM tile of (time tile, half): W rows [0, 128) from
+// W_B and [128, 256) from W_C, the half's 4 hs rows each (rows past them read the
+// half's first state: in a ragged last half the 8-row groups of a DMA instruction are
+// whole pairs of states, d_state being even); X rows the tile's tv tokens (rows past
+// the sequence read its last token).
+struct WRows {
+  const __bf16* wb;
+  const __bf16* wc;
+  int64_t row0;
+  int hs4, K;
+  __device__ const void* operator()(int g, int k0, int i, uint32_t& voff,
+                                    const DmaLane& dl) const {
+    voff = (uint32_t)(dl.lrow * K * 2) + dl.cb(i);
+    const int r = g & 127;  // 8-row groups never straddle B and C
+    const int rr = r < hs4 ? r : 0;
+    return (g < 128 ? wb : wc) + ((row0 + rr) * K + k0);
+  }
+};
+template <bool FULL_T>
+struct XRows {
+  const __bf16* x;
+  int64_t row0;
+  int tv, K;
+  __device__ const void* operator()(int g, int k0, int i, uint32_t& voff,
+                                    const DmaLane& dl) const {
+    if (FULL_T || tv == kT) {
+      voff = (uint32_t)(dl.lrow * K * 2) + dl.cb(i);
+      return x + ((row0 + g) * K + k0);
+    }
+    const int gb = g < tv ? g : tv - 1;
+    const int r = g + dl.lrow < tv ? g + dl.lrow : tv - 1;
+    voff = (uint32_t)((r - gb) * K * 2) + dl.cb(i);
+    return x + ((row0 + gb) * K + k0);
+  }
+};
 
 // The walk's and the epilogue's LDS addresses are the same for every tile; left to
 // itself the compiler computes them once and holds them (tens of registers) through
@@ -221,51 +261,42 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
   }
 
   const int n_tiles = (a.T + kT - 1) / kT;
-  for (int ti = 0; ti < n_tiles; ++ti) {
-    const int t0 = ti * kT;
-    const int tv = FULL_T ? kT : (a.T - t0 < kT ? a.T - t0 : kT);
-    const int64_t xrow0 = (int64_t)b * a.T + t0;
-    // This tile's delta and s, one token per thread of the first 256 (zero past the
-    // sequence: q = 1 and no input, so padded steps leave the state as it is). Stored
-    // to LDS once the first half's K loop has waited for them.
-    float dl_t = 0.f, s_t = 0.f;
+  auto wrows = [&](int h) {
+    const int hs = FULL_S ? kHalf : (S - h * kHalf < kHalf ? S - h * kHalf : kHalf);
+    return WRows{a.wb, a.wc, ((int64_t)d * S + h * kHalf) * 4, 4 * hs, K};
+  };
+  auto xrows = [&](int ti) {
+    const int tv = FULL_T ? kT : (a.T - ti * kT < kT ? a.T - ti * kT : kT);
+    return XRows<FULL_T>{a.x, (int64_t)b * a.T + ti * kT, tv, K};
+  };
+  // delta and s of time tile ti, one token per thread of the first 256 (zero past the
+  // sequence: q = 1 and no input, so padded steps leave the state as it is). Held in
+  // registers until the tile's first K loop has waited for them, then stored to LDS.
+  float dl_t = 0.f, s_t = 0.f;
+  auto load_ds = [&](int ti) {
+    const int tv = FULL_T ? kT : (a.T - ti * kT < kT ? a.T - ti * kT : kT);
+    dl_t = 0.f;
+    s_t = 0.f;
     if (tid < kT && tid < tv) {
-      const int64_t e = (xrow0 + tid) * a.Dm + d;
+      const int64_t e = ((int64_t)b * a.T + ti * kT + tid) * a.Dm + d;
       dl_t = io<bf16_t>::to_f32(a.delta[e]);
       s_t = io<bf16_t>::to_f32(a.s[e]);
     }
+  };
+  if (n_tiles > 0) load_ds(0);
+  for (int ti = 0; ti < n_tiles; ++ti) {
+    const int tv = FULL_T ? kT : (a.T - ti * kT < kT ? a.T - ti * kT : kT);
+    const int64_t xrow0 = (int64_t)b * a.T + ti * kT;
     for (int h = 0; h < NH; ++h) {
       // ---- 1. GEMM tile: rows [0, 128) of W_B, then [0, 128) of W_C, for the half's
-      // states; states past S read state 0's rows (their results are discarded).
-      const int64_t wrow0 = ((int64_t)d * S + h * kHalf) * 4;
+      // states, against the tile's tokens.
       const int hs = FULL_S ? kHalf : (S - h * kHalf < kHalf ? S - h * kHalf : kHalf);  // states in this half
       floatx4 acc[kWB][kXB];
 #pragma unroll
       for (int i = 0; i < kWB; ++i)
 #pragma unroll
         for (int j = 0; j < kXB; ++j) acc[i][j] = (floatx4){};
-      auto wrow = [&](int g, int k0, int i, uint32_t& voff, const DmaLane& dl) -> const void* {
-        voff = (uint32_t)(dl.lrow * K * 2) + dl.cb(i);
-        const int r = g & 127;  // 8-row groups never straddle B and C
-        const int rr = r < hs * 4 ? r : 0;
-        const __bf16* base = g < 128 ? a.wb : a.wc;
-        return base + ((wrow0 + rr) * K + k0);
-      };
-      auto xrow = [&](int g, int k0, int i, uint32_t& voff, const DmaLane& dl) -> const void* {
-        if (FULL_T || tv == kT) {
-          voff = (uint32_t)(dl.lrow * K * 2) + dl.cb(i);
-          return a.x + ((xrow0 + g) * K + k0);
-        }
-        // The ragged last tile: tokens past the sequence read its last token.
-        const int gb = g < tv ? g : tv - 1;
-        const int r = g + dl.lrow < tv ? g + dl.lrow : tv - 1;
-        voff = (uint32_t)((r - gb) * K * 2) + dl.cb(i);
-        return a.x + ((xrow0 + gb) * K + k0);
-      };
-      // In a ragged last half (d_state not a multiple of 32) the 8-row groups of a DMA
-      // instruction are two whole states (d_state is even), so clamping the group's
-      // base row keeps every lane's row inside the half.
-      tile_kloop(K, lds, acc, wrow, xrow);
+      tile_kloop(K, lds, acc, wrows(h), xrows(ti));
       if (h == 0 && tid < kT) *(float2*)(lds + kOffDS + tid * 8) = float2{dl_t, s_t};
 
       // ---- 2. The tile, rounded to bf16, over the stages (every wave is past its last
@@ -273,19 +304,19 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       wait_lgkm0();
       __builtin_amdgcn_s_barrier();
       {
-        // Cell of (t = wm * 64 + mb * 16 + rl, k = nb * 4 + q4): k ^ (t & 31) is
-        // (nb * 4) ^ ((mb & 1) * 16) ^ (q4 ^ rl), a constant per block XORed with the
-        // lane's x0.
-        const uint32_t base = opaque((uint32_t)((wm * 64 + rl) * kTokBytes + wn * 8));
+        // Cell of (t = wm * 64 + mb * 16 + rl, k = nb * 4 + q4) in the B (wn = 0) or C
+        // (wn = 1) tile: k ^ (t & 15) = (nb * 4) ^ (q4 ^ rl), a constant per block XORed
+        // with the lane's x0.
+        const uint32_t base = opaque((uint32_t)(wn * kOffC + (wm * 64 + rl) * kTokBytes));
         const uint32_t x0 = opaque((uint32_t)(q4 ^ rl));
 #pragma unroll
         for (int nb = 0; nb < kWB; ++nb)
 #pragma unroll
           for (int mb = 0; mb < kXB; ++mb) {
-            const uint32_t cst = (uint32_t)((nb * 4) ^ ((mb & 1) * 16));
+            const uint32_t cst = (uint32_t)(nb * 4);
             const floatx4& v = acc[nb][mb];
             const u32x2 pk = {pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])};
-            *(u32x2*)(lds + base + mb * 16 * kTokBytes + ((x0 ^ cst) << 4)) = pk;
+            *(u32x2*)(lds + base + mb * 16 * kTokBytes + ((x0 ^ cst) << 3)) = pk;
           }
       }
       wait_lgkm0();
@@ -310,14 +341,14 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       {
         quat hh{0.f, 0.f, 0.f, 0.f};
         float ca = 1.f, cb = 0.f;
-        // Token t = cA * 16 + j: t & 31 = (cA & 1) * 16 + j, so k ^ (t & 31) = kx ^ j.
+        // Token t = cA * 16 + j: t & 15 = j, so state k's cell is k ^ j.
         const uint32_t tb = opaque((uint32_t)(cA * kChunkLen));
-        const uint32_t kx = opaque((uint32_t)(kA ^ ((cA & 1) << 4)));
+        const uint32_t kx = opaque((uint32_t)kA);
 #pragma unroll
         for (int j = 0; j < kChunkLen; ++j) {
           const uint32_t t = tb + j;
           const float2 ds = *(const float2*)(lds + kOffDS + t * 8);
-          const u32x2 br = *(const u32x2*)(lds + t * kTokBytes + ((kx ^ j) << 4));
+          const u32x2 br = *(const u32x2*)(lds + t * kTokBytes + ((kx ^ j) << 3));
           const quat Bq{bf_lo(br[0]), bf_hi(br[0]), bf_lo(br[1]), bf_hi(br[1])};
           float c;
           const quat qq = cayley_step_c(ds.x, ds.x * ds.x, L, a.eps, c);
@@ -334,6 +365,11 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       }
       wait_lgkm0();
       __builtin_amdgcn_s_barrier();
+      // The next time tile's delta and s, loaded during the scan and the second pass.
+      // (Loading the next GEMM tile's first K stage into the B tile here, LDS stage 0,
+      // which the walk has read by now, measured no faster: 16.48-16.61 against
+      // 16.45-16.46 ms at config 3, same box.)
+      if (h + 1 == NH && ti + 1 < n_tiles) load_ds(ti + 1);
 
       // ---- 3b. Start states: an inclusive scan over each state's 16 chunks (row shifts
       // of 1, 2, 4, 8 within the 16-lane row), the carried state folded into chunk 0.
@@ -387,11 +423,11 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
         float o[4 * kChunkLen];
         const bool live = FULL_S || kA < hs;
         const uint32_t tb = opaque((uint32_t)(cA * kChunkLen));
-        const uint32_t kx = opaque((uint32_t)(kA ^ ((cA & 1) << 4)));
+        const uint32_t kx = opaque((uint32_t)kA);
 #pragma unroll
         for (int j = 0; j < kChunkLen; ++j) {
           const uint32_t t = tb + j;
-          const u32x2 r = *(const u32x2*)(lds + t * kTokBytes + ((kx ^ j) << 4) + 8);
+          const u32x2 r = *(const u32x2*)(lds + kOffC + t * kTokBytes + ((kx ^ j) << 3));
           const quat Cq{bf_lo(r[0]), bf_hi(r[0]), bf_lo(r[1]), bf_hi(r[1])};
           const quat hh{fmaf(pa[j], hs0.w, fmaf(pb[j], vh.w, hl[j].w)),
                         fmaf(pa[j], hs0.x, fmaf(pb[j], vh.x, hl[j].x)),

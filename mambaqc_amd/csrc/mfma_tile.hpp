@@ -128,6 +128,34 @@ static_assert(Tile256::WB == kWB && Tile256::XB == kXB && Tile256::kStagesBytes 
 //          swizzle), row pitch ld * 2 bytes; the caller may clamp rows past the matrix.
 // Returns after the last MFMA; the caller waits on lgkmcnt and barriers before reusing
 // the LDS stages.
+// LDS address of the dynamic LDS array (for the DMA's M0).
+__device__ inline uint32_t lds_addr(char* lds) { return (uint32_t)(uintptr_t)(lds_void_t*)lds; }
+
+// The DMA of K stage kt (into LDS stage kt & 1) for the K loop below; wave is the
+// (wave-uniform) wave index, dl the lane's DmaLane and lds0 = lds_addr(lds).
+template <typename Cfg, typename WRow, typename XRow>
+__device__ inline void tile_issue_stage(int kt, int wave, uint32_t lds0, const DmaLane& dl,
+                                        const WRow& wrow, const XRow& xrow) {
+  const int k0 = kt * kBK;
+  const uint32_t sb = lds0 + (uint32_t)((kt & 1) * Cfg::kStageBytes);
+  constexpr int NL = Cfg::kWLoads > Cfg::kXLoads ? Cfg::kWLoads : Cfg::kXLoads;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    if (i < Cfg::kWLoads) {
+      const int gi = wave * Cfg::kWLoads + i;
+      uint32_t wv;
+      const void* wb = wrow(gi * kRowsPerLoad, k0, gi, wv, dl);
+      dma16(wb, wv, sb + (uint32_t)(gi * 1024));
+    }
+    if (i < Cfg::kXLoads) {
+      const int gi = wave * Cfg::kXLoads + i;
+      uint32_t xv;
+      const void* xb = xrow(gi * kRowsPerLoad, k0, gi, xv, dl);
+      dma16(xb, xv, sb + (uint32_t)(Cfg::kWBytes + gi * 1024));
+    }
+  }
+}
+
 template <typename Cfg, typename WRow, typename XRow>
 __device__ inline void tile_kloop_cfg(int K, char* lds,
                                       floatx4 (&acc)[Cfg::WB][Cfg::XB], const WRow& wrow,
@@ -137,27 +165,8 @@ __device__ inline void tile_kloop_cfg(int K, char* lds,
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const DmaLane dl(lane);
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)lds;
-  auto issue_stage = [&](int kt) {
-    const int k0 = kt * kBK;
-    const uint32_t sb = lds0 + (uint32_t)((kt & 1) * Cfg::kStageBytes);
-    constexpr int NL = Cfg::kWLoads > Cfg::kXLoads ? Cfg::kWLoads : Cfg::kXLoads;
-#pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      if (i < Cfg::kWLoads) {
-        const int gi = wave * Cfg::kWLoads + i;
-        uint32_t wv;
-        const void* wb = wrow(gi * kRowsPerLoad, k0, gi, wv, dl);
-        dma16(wb, wv, sb + (uint32_t)(gi * 1024));
-      }
-      if (i < Cfg::kXLoads) {
-        const int gi = wave * Cfg::kXLoads + i;
-        uint32_t xv;
-        const void* xb = xrow(gi * kRowsPerLoad, k0, gi, xv, dl);
-        dma16(xb, xv, sb + (uint32_t)(Cfg::kWBytes + gi * 1024));
-      }
-    }
-  };
+  const uint32_t lds0 = lds_addr(lds);
+  auto issue_stage = [&](int kt) { tile_issue_stage<Cfg>(kt, wave, lds0, dl, wrow, xrow); };
 
   const int wn = wave / Cfg::NW_X;
   const int wm = wave % Cfg::NW_X;
