@@ -255,9 +255,33 @@ def box_copy_gbs(reps=20):
 FUSED_STAGE = "fused B/C projections + SSM (mqc_ssm_fused_bc_fwd)"
 
 
+def flushed_time_ms(fn, reps):
+    """Median duration of fn() over reps calls, each after a 1 GiB device copy
+    that evicts L2 and the Infinity Cache; the copy occupies the device while fn's
+    launches are queued, so the events around fn time its kernels, not the host."""
+    import torch
+
+    src = torch.empty(1 << 28, device="cuda")
+    dst = torch.empty_like(src)
+    fn()
+    ts = []
+    for _ in range(reps):
+        dst.copy_(src)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    del src, dst
+    return sorted(ts)[len(ts) // 2]
+
+
 def run_full(args):
     import torch
     from mambaqc_amd import kernels as K
+    from mambaqc_amd.block import _out_proj, out_gate, out_proj_gate
 
     dtype = torch.bfloat16
     # Measured first, on a cold device, like the standalone copy mode.
@@ -315,18 +339,36 @@ def run_full(args):
         stages["B_proj GEMM mqc_gemm_nt (MFMA, this library)"] = event_time_ms(
             lambda: mqc_gemm(xa, wb, gemm_out), 5)
         del gemm_out, xa
-        # The block's two inference paths for the B/C projections, same block and
-        # input: fused into the SSM kernel (the default at this size) and unfused
-        # (hipBLASLt GEMMs, then the SSM kernel).
-        stages["block forward (default: B/C fused into the SSM, fused output step)"] = \
-            event_time_ms(lambda: blk(x), 5)
-        blk.fuse_bc = False
-        stages["block forward, B/C unfused (hipBLASLt + SSM)"] = event_time_ms(lambda: blk(x), 5)
-        blk.fuse_bc = None
-        blk.fuse_out = False
-        stages["block forward, output step unfused (out_proj + gate kernel)"] = \
-            event_time_ms(lambda: blk(x), 5)
-        blk.fuse_out = None
+        # The block's inference paths on the same block and input, interleaved
+        # (median over rounds): the default (B/C projections fused into the SSM
+        # kernel, output step as out_proj then the gate kernel), B/C unfused
+        # (hipBLASLt GEMMs, then the SSM kernel), and the output step fused.
+        variants = {
+            "block forward (default: B/C fused into the SSM)": (None, None),
+            "block forward, B/C unfused (hipBLASLt + SSM)": (False, None),
+            "block forward, output step fused (mqc_out_proj_gate_fwd)": (None, True),
+        }
+        ab = {k: [] for k in variants}
+        for _ in range(4):
+            for name, (fbc, fout) in variants.items():
+                blk.fuse_bc, blk.fuse_out = fbc, fout
+                blk(x)
+                ab[name].append(event_time_ms(lambda: blk(x), 3))
+        blk.fuse_bc = blk.fuse_out = None
+        for name, v in ab.items():
+            stages[name] = sorted(v)[len(v) // 2]
+        # The output step alone, fused and unfused, each call after a 1 GiB copy
+        # that evicts its operands from the caches (as in the block, where the SSM's
+        # traffic has evicted them); the copy keeps the device busy while the step
+        # is queued, so the events time the step's kernels only.
+        yq = blk.norm(K.ssm_forward_fused_bc(xa_in, wbf, wcf, delta, s, la, li, Dv, eps=1e-6))
+        zq = torch.randn(B, T, 2 * DI, generator=g, device="cuda").to(dtype)[..., DI:]
+        ow = blk.out_proj.weight.detach()
+        stages["output step fused (mqc_out_proj_gate_fwd), caches flushed"] = flushed_time_ms(
+            lambda: out_proj_gate(x, zq, yq, ow), 10)
+        stages["output step unfused (out_proj + gate kernel), caches flushed"] = flushed_time_ms(
+            lambda: out_gate(x, zq, _out_proj(blk.out_proj, yq)), 10)
+        del yq, zq
         # The d-sliced B/C path on the same block and input (96 d's per slice:
         # 16 slices of two GEMMs and one chunked SSM each) against the whole
         # projections the block uses at this size.

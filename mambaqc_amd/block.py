@@ -195,10 +195,13 @@ BC_SLICE_BYTES = 2 << 30
 # on chip and never stored. Shorter sequences (a decode step, short prompts) would
 # fill one tile with a few tokens and keep the separate GEMMs.
 FUSED_BC_MIN_SEQ = 256
-# bf16 inference with at least this many token rows runs the output step (out_proj +
-# gate + residual) as one kernel (mqc_out_proj_gate_fwd); decode-sized steps keep the
-# skinny GEMM and the gate kernel.
-FUSED_OUT_MIN_ROWS = 1024
+# The output step (out_proj + gate + residual) as one kernel (mqc_out_proj_gate_fwd) is
+# opt-in (fuse_out=True). Back to back on operands resident in the chip's caches it beats
+# out_proj (hipBLASLt) + the gate kernel at the config-3 shape (76.5 against 79.3 us), but
+# inside the block its operands come from HBM: y just written, W, x and z evicted by the
+# SSM's traffic, and there its two 28 KB stages per workgroup leave the K loop waiting on
+# HBM latency (115-122 against 97-105 us with the caches flushed before each call;
+# 109 against 92 us in a trace of the block).
 
 
 def bc_slice_width(batch: int, seq_len: int, d_inner: int, d_state: int, elsize: int,
@@ -383,9 +386,9 @@ class QuaternionMamba2Block(nn.Module):
     d_state <= 64) and sequences have at least FUSED_BC_MIN_SEQ tokens; True
     also for shorter ones; False never. A forced bc_slice_d takes precedence.
 
-    fuse_out (attribute): None runs the output step of bf16 inference (out_proj,
-    gate, residual) as one kernel (out_proj_gate) from FUSED_OUT_MIN_ROWS token
-    rows on; True for any number of rows; False never.
+    fuse_out (attribute): True runs the output step of bf16 inference (out_proj,
+    gate, residual) as one kernel (out_proj_gate) where it applies; None (the
+    default) and False run out_proj, then out_gate.
     """
 
     def __init__(self, d_model: int, d_state: int = 64, d_conv: int = 4,
@@ -427,10 +430,9 @@ class QuaternionMamba2Block(nn.Module):
         """x + sigmoid(z[..., :d_model]) * out_proj(y): one fused launch for bf16
         inference where it applies (fuse_out), else out_proj then out_gate."""
         op = self.out_proj
-        if (self.fuse_out is not False and not nat.compiling()
+        if (self.fuse_out and not nat.compiling()
                 and not (torch.is_grad_enabled() and (y.requires_grad or x.requires_grad
                                                       or op.weight.requires_grad))
-                and (self.fuse_out or x.numel() // max(x.shape[-1], 1) >= FUSED_OUT_MIN_ROWS)
                 and out_proj_gate_eligible(x, z, y, op.weight, op.bias)):
             return out_proj_gate(x, z, y, op.weight, op.bias)
         return out_gate(x, z, _out_proj(op, y))

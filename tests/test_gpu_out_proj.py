@@ -78,17 +78,17 @@ def test_out_proj_gate_rejects_what_it_cannot_run():
 
 
 def test_block_output_step_fused_vs_unfused():
-    """The block's output step takes the fused kernel for bf16 inference from
-    FUSED_OUT_MIN_ROWS rows on (fuse_out None) or always (True); both against the
-    unfused step (False) on the same block and input."""
+    """The block's output step takes the fused kernel for bf16 inference when
+    fuse_out is True; against the unfused step (the default, None) on the same
+    block and input."""
     torch.manual_seed(2)
     blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=16).to(DEV, BF).eval()
     x = torch.randn(2, 520, 64, generator=torch.Generator(device=DEV).manual_seed(3),
                     device=DEV).to(BF)
     with torch.no_grad():
-        got = blk(x)
-        blk.fuse_out = False
         ref = blk(x)
+        blk.fuse_out = True
+        got = blk(x)
         blk.fuse_out = True
         small = blk(x[:, :7])
         blk.fuse_out = False
