@@ -211,14 +211,14 @@ def cpu_components():
     return out
 
 
-def read_traffic():
-    """HBM bytes per launch of the SSM kernel from the committed rocprofv3 PMC
+def read_traffic(name="ssm_fused_fwd_c3_traffic.txt", key="traffic_bytes_per_launch:"):
+    """Bytes per launch leaving the L2 for a kernel, from a committed rocprofv3 PMC
     summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor)."""
-    p = ROOT / "profiles" / "ssm_fused_fwd_c3_traffic.txt"
+    p = ROOT / "profiles" / name
     if not p.exists():
         return None
     for line in p.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
+        if line.startswith(key):
             return float(line.split(":", 1)[1])
     return None
 
@@ -451,6 +451,7 @@ def run_full(args):
             "unit": "TFLOP/s",
             "frac": round(2 * gemm_flop / (stages[FUSED_STAGE] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
             "flop": 2 * gemm_flop,
+            "traffic": read_traffic("fused_bc_ssm_c3.txt", "fused_traffic_bytes_per_launch:"),
             "mean_launch_ms": round(stages[FUSED_STAGE], 4),
             "hipblaslt_B_proj_TFLOPs": round(
                 gemm_flop / (stages["B_proj GEMM hipBLASLt (column blocks)"] * 1e-3) / 1e12, 1),

@@ -45,7 +45,8 @@ extern "C" {
 #define MQC_E_SPACE (-6)     /* a workspace is smaller than the call needs */
 #define MQC_E_OVERLAP (-7)   /* an output overlaps an input that the launch still reads
                               * (the chunked SSM walks: h_last over h0, dh0 over
-                              * dh_last) */
+                              * dh_last; every SSM walk: h_last sharing bytes with h0
+                              * without being the same buffer) */
 
 /* Human-readable text for a status code (static storage, never NULL). */
 const char* mqc_status_string(int status);
@@ -92,7 +93,8 @@ int mqc_cumprod_scan_fwd(const void* q, void* out, int64_t batch, int64_t seq_le
  * [d_inner] vector needs no copy); h0: dtype [batch, d_inner, d_state, 4] or
  * NULL for zeros; y: dtype [batch, seq_len, d_inner, 4]; h_last: dtype
  * [batch, d_inner, d_state, 4] or NULL. With seq_len 0, h_last (if given)
- * receives h0, or zeros, and the per-step operands may be NULL.
+ * receives h0, or zeros, and the per-step operands may be NULL. h_last may be
+ * h0; buffers that overlap without being the same are refused (MQC_E_OVERLAP).
  * Replaces ssm_forward_fused, mambaqc/kernels/ssm_fused.py:340-401, and (with
  * seq_len = 1, h0 = h_prev, h_last = h_new) ssm_step_fused, :258-337. */
 int mqc_ssm_q_fwd(const void* q, const void* B, const void* S, const void* C, const void* D,
@@ -116,7 +118,8 @@ int mqc_ssm_q_fwd(const void* q, const void* B, const void* S, const void* C, co
  * receives h0, or zeros; delta, s, B, C and y may then be NULL, the
  * parameters may not. h_last may be h0 (the state updated in place, as the
  * recurrent decode does): each state is written only by the lane that read it,
- * after its walk.
+ * after its walk. Buffers that overlap without being the same are refused
+ * (MQC_E_OVERLAP).
  * Replaces the body of QuaternionMamba2Block._ssm_forward,
  * mambaqc/models/quaternion_mamba2_block.py:206-228 (Lambda, z = delta*Lambda,
  * cayley_discretization_fused, ssm_forward_fused), without materialising z or q. */
@@ -202,7 +205,8 @@ int mqc_ssm_noalloc_prepare(void);
  * (the projections' input, 16-byte aligned); B_weight, C_weight: [d_inner * d_state * 4,
  * d_inner] (nn.Linear layout, 16-byte aligned); delta, s: [batch, seq_len, d_inner];
  * the parameters, h0, y and h_last as in mqc_ssm_fused_fwd (y 8-byte aligned, h0 and
- * h_last 16-byte aligned; h_last may be h0). d_inner a multiple of 64; d_state even,
+ * h_last 16-byte aligned; h_last may be h0, a partial overlap is refused with
+ * MQC_E_OVERLAP). d_inner a multiple of 64; d_state even,
  * at most 64. Replaces B_proj/C_proj (F.linear, mambaqc/layers/quaternion_linear.py:145-161,
  * called at mambaqc/models/quaternion_mamba2_block.py:186-191) together with the SSM
  * they feed (quaternion_mamba2_block.py:206-228). */

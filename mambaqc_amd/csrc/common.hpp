@@ -270,4 +270,11 @@ inline bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
   return x < y + (uintptr_t)nb && y < x + (uintptr_t)na;
 }
 
+// Two state buffers of n bytes that share bytes without being the same buffer:
+// where a kernel allows h_last == h0 (each state written only by the lane that
+// read it), a shifted alias still lets one lane overwrite another's h0 first.
+inline bool partial_overlap(const void* a, const void* b, int64_t n) {
+  return a != b && overlaps(a, n, b, n);
+}
+
 }  // namespace mqc

@@ -513,7 +513,9 @@ int mqc_ssm_fused_bc_fwd(const void* x, const void* B_weight, const void* C_weig
   if (batch * d_inner > 0x7fffffffLL || batch * seq_len > (1LL << 30) || d_inner > (1 << 20))
     return MQC_E_LIMIT;
   // Each (b, d) reads h0 and writes h_last for its own states only, after its walk:
-  // h_last may be h0.
+  // h_last may be h0, but not a shifted alias of it.
+  if (partial_overlap(h0, h_last, batch * d_inner * d_state * 4 * (int64_t)sizeof(float)))
+    return MQC_E_OVERLAP;
   if (seq_len == 0 && !h_last) return MQC_OK;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);

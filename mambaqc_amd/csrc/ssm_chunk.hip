@@ -94,6 +94,7 @@ int check_chunked(const void* delta, const void* s, const void* B, const void* C
   const int64_t state_bytes = batch * d_inner * d_state * 4 * (int64_t)sizeof(float);
   if (steps && seq_len > chunk_len && overlaps(h0, state_bytes, h_last, state_bytes))
     return MQC_E_OVERLAP;
+  if (partial_overlap(h0, h_last, state_bytes)) return MQC_E_OVERLAP;
   return MQC_OK;
 }
 

@@ -31,6 +31,8 @@ int mqc_ssm_q_fwd(const void* q, const void* B, const void* S, const void* C, co
   if (steps && d_state == 0) return MQC_E_SHAPE;
   if (steps && (!q || !B || !S || !C || !D || !y)) return MQC_E_NULL;
   if (batch > 65535 || d_inner > (1LL << 24) || d_state > 256) return MQC_E_LIMIT;
+  const int64_t elsize = dtype == MQC_F32 ? 4 : 2;
+  if (partial_overlap(h0, h_last, batch * d_inner * d_state * 4 * elsize)) return MQC_E_OVERLAP;
   SsmArgs a{};
   a.q = q; a.Sq = S; a.Dq = D; a.d_sb = d_sb; a.d_st = d_st; a.d_sd = d_sd;
   a.Bm = B; a.Cm = C; a.h0 = h0; a.y = y; a.h_last = h_last;
@@ -52,6 +54,8 @@ int mqc_ssm_fused_fwd(const void* delta, const void* s, const void* B, const voi
   if (steps && (!delta || !s || !B || !C || !y)) return MQC_E_NULL;
   if ((steps || state_only) && (!lambda_alpha || !lambda_imag || !D)) return MQC_E_NULL;
   if (batch > 65535 || d_inner > (1LL << 24) || d_state > 256) return MQC_E_LIMIT;
+  if (partial_overlap(h0, h_last, batch * d_inner * d_state * 4 * (int64_t)sizeof(float)))
+    return MQC_E_OVERLAP;
   SsmArgs a{};
   a.delta = delta; a.s = s; a.lam_alpha = lambda_alpha; a.lam_imag = lambda_imag; a.dvec = D;
   a.Bm = B; a.Cm = C; a.h0 = h0; a.y = y; a.h_last = h_last;

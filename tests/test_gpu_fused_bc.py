@@ -160,9 +160,10 @@ def test_fused_bc_rejects_what_it_cannot_run():
 
 def test_block_forward_fused_bc_path():
     """QuaternionMamba2Block inference in bf16 takes the fused path from
-    FUSED_BC_MIN_SEQ tokens on: its output against the same block with fusion off
-    and against the CPU oracle of the block (fp32 on the same bf16 weights), and a
-    sequence fed in two pieces through forward_with_state against the whole."""
+    FUSED_BC_MIN_SEQ tokens and FUSED_BC_MIN_BATCH sequences on: its output against
+    the same block with fusion off and against the CPU oracle of the block (fp32 on
+    the same bf16 weights), and a sequence fed in two pieces through
+    forward_with_state against the whole."""
     import mambaqc_amd
     from mambaqc_amd import block as blockmod
 
@@ -172,6 +173,12 @@ def test_block_forward_fused_bc_path():
     x = torch.randn(2, 300, 64, generator=g, device=DEV).to(BF)
     assert x.shape[1] >= blockmod.FUSED_BC_MIN_SEQ and blk._use_fused_bc(
         torch.empty(2, 300, blk.d_inner, device=DEV, dtype=BF))
+    # A batch of one keeps the unfused path unless fusion is forced.
+    one = torch.empty(1, 300, blk.d_inner, device=DEV, dtype=BF)
+    assert blockmod.FUSED_BC_MIN_BATCH == 2 and not blk._use_fused_bc(one)
+    blk.fuse_bc = True
+    assert blk._use_fused_bc(one)
+    blk.fuse_bc = None
     with torch.no_grad():
         got = blk(x)
         blk.fuse_bc = False

@@ -231,6 +231,27 @@ def test_chunked_walks_refuse_in_place_state_without_gpu():
                                          H, b, T, d, k, Lk, 1e-6, 1, FAKE, need_k, None) == -7
 
 
+def test_whole_walks_refuse_shifted_state_alias_without_gpu():
+    """The whole walks and the fused B/C walk take h_last == h0, but refuse state
+    buffers that share bytes without being the same buffer (one lane could then
+    overwrite another's h0 before it is read): MQC_E_OVERLAP before any HIP call."""
+    lib = nat.load()
+    b, T, d, k = 1, 100, 64, 8
+    nbytes = b * d * k * 16
+    H = ctypes.c_void_p(1 << 20)
+    H_part = ctypes.c_void_p((1 << 20) + nbytes - 16)
+    # (delta, s, B, C, lambda_alpha, lambda_imag, D, h0, y, h_last, b, T, d, k, eps, dtype, stream)
+    assert lib.mqc_ssm_fused_fwd(*[FAKE] * 7, H, FAKE, H_part, b, T, d, k, 1e-6, 1, None) == -7
+    # (q, B, S, C, D, d_sb, d_st, d_sd, h0, y, h_last, b, T, d, k, dtype, stream): bf16
+    # state, 8 bytes per quaternion.
+    H_half = ctypes.c_void_p((1 << 20) + nbytes // 2 - 8)
+    assert lib.mqc_ssm_q_fwd(*[FAKE] * 5, 0, 0, 0, H, FAKE, H_half, b, T, d, k, 1, None) == -7
+    # (x, W_B, W_C, delta, s, lambda_alpha, lambda_imag, D, h0, y, h_last, b, T, d, k, eps,
+    #  dtype, stream)
+    assert lib.mqc_ssm_fused_bc_fwd(*[FAKE] * 8, H, FAKE, H_part, b, T, d, k, 1e-6, 1,
+                                    None) == -7
+
+
 def test_fused_bc_validation_without_gpu():
     """mqc_ssm_fused_bc_fwd refuses, before any HIP call: a dtype other than bf16,
     d_state odd or above 64, d_inner not a multiple of 64, NULL operands and
