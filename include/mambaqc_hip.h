@@ -216,6 +216,30 @@ int mqc_ssm_fused_bc_fwd(const void* x, const void* B_weight, const void* C_weig
                          void* h_last, int64_t batch, int64_t seq_len, int64_t d_inner,
                          int64_t d_state, float eps, int dtype, void* stream);
 
+/* Bytes of workspace mqc_ssm_fused_bc_fwd_split needs for these sizes: the two
+ * halves' fp32 partial sums of y, 2 * batch * seq_len * d_inner * 16; 0 when there is
+ * one half of states (d_state <= 32) or nothing to walk. Negative: an MQC_E_* code. */
+int64_t mqc_ssm_fused_bc_split_workspace_bytes(int64_t batch, int64_t seq_len,
+                                               int64_t d_inner, int64_t d_state);
+
+/* mqc_ssm_fused_bc_fwd with each half of the states (32) in a workgroup of its own,
+ * for batches too small to share the weight rows: a workgroup per (b, d) streams its
+ * d's 512 weight rows once per 256-token tile, the workgroups of a d's batches share
+ * those reads in L2, and a single sequence's resident d's want more weight rows than the
+ * Infinity Cache holds; per half they want half as many. Each half writes its fp32
+ * partial sum of y to the workspace (at least
+ * mqc_ssm_fused_bc_split_workspace_bytes, 16-byte aligned, owned by the caller, no
+ * contents needed on entry) and a second launch adds them with D s, in the order the
+ * one-launch form does: y equals mqc_ssm_fused_bc_fwd's bit for bit. With one half of
+ * states the call is mqc_ssm_fused_bc_fwd (workspace unused, may be NULL). Same
+ * arguments, limits and replaced reference lines as mqc_ssm_fused_bc_fwd. */
+int mqc_ssm_fused_bc_fwd_split(const void* x, const void* B_weight, const void* C_weight,
+                               const void* delta, const void* s, const float* lambda_alpha,
+                               const float* lambda_imag, const float* D, const void* h0,
+                               void* y, void* h_last, int64_t batch, int64_t seq_len,
+                               int64_t d_inner, int64_t d_state, float eps, int dtype,
+                               void* workspace, int64_t workspace_bytes, void* stream);
+
 /* The block's output step in one launch, bf16 only (dtype MQC_BF16):
  *   out[r, n] = x[r, n] + sigmoid(z[r, n]) * bf16(sum_j y[r, j] W[n, j] + bias[n])
  * for r < rows, n < d_model: the quaternion -> real projection out_proj of the

@@ -71,6 +71,8 @@ SIGNATURES = {
     "mqc_ssm_noalloc_prepare": [],
     "mqc_ssm_fused_bc_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                              _i64, _i64, _i64, _i64, _f32, _int, _vp],
+    "mqc_ssm_fused_bc_fwd_split": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                   _i64, _i64, _i64, _i64, _f32, _int, _vp, _i64, _vp],
     "mqc_out_proj_gate_fwd": [_vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _int, _vp],
 }
 
@@ -80,9 +82,10 @@ SIGNATURES_I64 = {
     "mqc_ssm_chunk_len_auto": [_i64, _i64, _i64, _i64, _int],
     "mqc_ssm_chunked_workspace_bytes": [_i64, _i64, _i64, _i64, _i64],
     "mqc_ssm_chunked_scratch_bytes": [],
+    "mqc_ssm_fused_bc_split_workspace_bytes": [_i64, _i64, _i64, _i64],
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib = None

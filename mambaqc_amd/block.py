@@ -190,17 +190,16 @@ def _rows_uniform(z: torch.Tensor) -> bool:
 BC_WHOLE_MAX_BYTES = 32 << 30
 BC_SLICE_BYTES = 2 << 30
 
-# Inference in bf16 from this many tokens per sequence and sequences per batch on: the
-# B/C projections and the SSM run as one kernel (mqc_ssm_fused_bc_fwd), B and C computed
-# in 256-token tiles on chip and never stored. Shorter sequences (a decode step, short
-# prompts) would fill one tile with a few tokens and keep the separate GEMMs. A batch of
-# one keeps them too: the kernel's workgroup per (sequence, d) re-reads its d's weight rows
-# for every tile, and the sequences of a batch share those reads in L2; alone, one
-# sequence streams the weights 8 times per 2048 tokens. Block forward at the config-3
-# width, fused against unfused: B1 T2048 5.45 / 4.86 ms, B1 T16384 43.4 / 35.5 ms;
-# B2 T2048 8.42 / 9.09 ms, B2 T16384 65.6 / 71.0 ms, B4 T2048 16.36 / 17.03 ms.
+# Inference in bf16 from this many tokens per sequence on: the B/C projections and the
+# SSM run as one kernel (mqc_ssm_fused_bc_fwd), B and C computed in 256-token tiles on
+# chip and never stored. Shorter sequences (a decode step, short prompts) would fill one
+# tile with a few tokens and keep the separate GEMMs. A batch of one runs the kernel with
+# each half of the states in a workgroup of its own (ssm_forward_fused_bc's split), since
+# one workgroup per d would re-stream more weight rows than the Infinity Cache holds.
+# Block forward at the config-3 width, fused against unfused (one box): B1 T2048 4.63 /
+# 4.91 ms, B1 T4096 9.00 / 9.47, B1 T16384 36.5 / 35.8, B1 T65536 145.3 / 144.5 (sliced);
+# B2 T2048 8.81 / 9.16, B4 T2048 16.98 / 17.33 (one workgroup per d: B1 T2048 5.45 ms).
 FUSED_BC_MIN_SEQ = 256
-FUSED_BC_MIN_BATCH = 2
 # The output step (out_proj + gate + residual) as one kernel (mqc_out_proj_gate_fwd) is
 # opt-in (fuse_out=True). Back to back on operands resident in the chip's caches it beats
 # out_proj (hipBLASLt) + the gate kernel at the config-3 shape (76.5 against 79.3 us), but
@@ -389,8 +388,7 @@ class QuaternionMamba2Block(nn.Module):
     fuse_bc (attribute): None runs inference (no autograd) with the B/C
     projections fused into the SSM kernel (ssm_forward_fused_bc) where that
     kernel applies (bf16, bias-free projections, d_inner a multiple of 64, even
-    d_state <= 64), sequences have at least FUSED_BC_MIN_SEQ tokens and batches at
-    least FUSED_BC_MIN_BATCH sequences; True
+    d_state <= 64) and sequences have at least FUSED_BC_MIN_SEQ tokens; True
     also for shorter ones; False never. A forced bc_slice_d takes precedence.
 
     fuse_out (attribute): True runs the output step of bf16 inference (out_proj,
@@ -530,8 +528,7 @@ class QuaternionMamba2Block(nn.Module):
             return False
         if torch.is_autocast_enabled(x.device.type):
             return False
-        if self.fuse_bc is None and (x.shape[1] < FUSED_BC_MIN_SEQ
-                                     or x.shape[0] < FUSED_BC_MIN_BATCH):
+        if self.fuse_bc is None and x.shape[1] < FUSED_BC_MIN_SEQ:
             return False
         return fused_bc_eligible(x, self.B_proj.weight, self.C_proj.weight, self.d_state)
 

@@ -77,7 +77,9 @@ struct FusedArgs {
   const float* h0;         // [batch, d_inner, S, 4] or null
   __bf16* y;               // [batch, T, d_inner, 4]
   float* h_last;           // [batch, d_inner, S, 4] or null
+  float* ypart;            // split: y's partial sums [halves, batch, T, d_inner, 4]
   int batch, T, Dm, S;
+  int split;               // one workgroup per (b, d, half) instead of per (b, d)
   float eps;
 };
 
@@ -226,16 +228,22 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
   const int rl = lane & 15;
   const int q4 = lane >> 4;
 
-  // Unit (b, d): logical order d-major with the batches adjacent, each XCD a
-  // contiguous range of it (blocks go to the XCDs round-robin by linear id).
+  // Unit (b, d), or (b, d, half) when split: logical order d-major (then the half)
+  // with the batches adjacent, each XCD a contiguous range of it (blocks go to the
+  // XCDs round-robin by linear id).
   const int n = (int)gridDim.x;
   const int lin = (int)blockIdx.x;
   const int logical = n % kXCDs ? lin : (lin % kXCDs) * (n / kXCDs) + lin / kXCDs;
-  const int d = __builtin_amdgcn_readfirstlane(logical / a.batch);
-  const int b = __builtin_amdgcn_readfirstlane(logical - d * a.batch);
   const int K = a.Dm;
   const int S = a.S;
   const int NH = (S + kHalf - 1) / kHalf;
+  const int per_d = a.split ? a.batch * NH : a.batch;
+  const int d = __builtin_amdgcn_readfirstlane(logical / per_d);
+  const int rem = logical - d * per_d;
+  const int hsel = __builtin_amdgcn_readfirstlane(a.split ? rem / a.batch : 0);
+  const int b = __builtin_amdgcn_readfirstlane(rem - hsel * a.batch);
+  const int h_begin = a.split ? hsel : 0;
+  const int h_end = a.split ? hsel + 1 : NH;
   const int64_t bd = (int64_t)b * a.Dm + d;
 
   // Walk mapping A: state kA of the half, chunk cA (tokens cA * 16 + [0, 16)).
@@ -287,7 +295,7 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
   for (int ti = 0; ti < n_tiles; ++ti) {
     const int tv = FULL_T ? kT : (a.T - ti * kT < kT ? a.T - ti * kT : kT);
     const int64_t xrow0 = (int64_t)b * a.T + ti * kT;
-    for (int h = 0; h < NH; ++h) {
+    for (int h = h_begin; h < h_end; ++h) {
       // ---- 1. GEMM tile: rows [0, 128) of W_B, then [0, 128) of W_C, for the half's
       // states, against the tile's tokens.
       const int hs = FULL_S ? kHalf : (S - h * kHalf < kHalf ? S - h * kHalf : kHalf);  // states in this half
@@ -297,7 +305,7 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
 #pragma unroll
         for (int j = 0; j < kXB; ++j) acc[i][j] = (floatx4){};
       tile_kloop(K, lds, acc, wrows(h), xrows(ti));
-      if (h == 0 && tid < kT) *(float2*)(lds + kOffDS + tid * 8) = float2{dl_t, s_t};
+      if (h == h_begin && tid < kT) *(float2*)(lds + kOffDS + tid * 8) = float2{dl_t, s_t};
 
       // ---- 2. The tile, rounded to bf16, over the stages (every wave is past its last
       // fragment read at the barrier).
@@ -369,7 +377,7 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       // (Loading the next GEMM tile's first K stage into the B tile here, LDS stage 0,
       // which the walk has read by now, measured no faster: 16.48-16.61 against
       // 16.45-16.46 ms at config 3, same box.)
-      if (h + 1 == NH && ti + 1 < n_tiles) load_ds(ti + 1);
+      if (h + 1 == h_end && ti + 1 < n_tiles) load_ds(ti + 1);
 
       // ---- 3b. Start states: an inclusive scan over each state's 16 chunks (row shifts
       // of 1, 2, 4, 8 within the 16-lane row), the carried state folded into chunk 0.
@@ -445,7 +453,7 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
         const int i0 = ((u & 16) ? 0 : 32) + 2 * (u & 15);
         const int t = cA * kChunkLen + (i0 >> 2);
         float2* yp = (float2*)(lds + kOffY + t * 16 + (i0 & 3) * 4);
-        if (h == 0) {
+        if (h == h_begin) {
           *yp = float2{r0, r1};
         } else {
           const float2 prev = *yp;
@@ -456,20 +464,46 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       wait_lgkm0();
       __builtin_amdgcn_s_barrier();
     }
-    // ---- 4. y of the tile.
+    // ---- 4. y of the tile, or (split) this half's partial sum of it.
     if (tid < tv) {
-      const float dsk = a.dvec[d];
       const float4 yv = *(const float4*)(lds + kOffY + tid * 16);
-      const float sv = (*(const float2*)(lds + kOffDS + tid * 8)).y;
-      const u32x2 pk = {pk_bf16(fmaf(dsk, sv, yv.x), yv.y), pk_bf16(yv.z, yv.w)};
-      *(u32x2*)(a.y + ((xrow0 + tid) * a.Dm + d) * 4) = pk;
+      if (a.split) {
+        const int64_t row = (int64_t)hsel * a.batch * a.T + xrow0 + tid;
+        *(float4*)(a.ypart + (row * a.Dm + d) * 4) = yv;
+      } else {
+        const float dsk = a.dvec[d];
+        const float sv = (*(const float2*)(lds + kOffDS + tid * 8)).y;
+        const u32x2 pk = {pk_bf16(fmaf(dsk, sv, yv.x), yv.y), pk_bf16(yv.z, yv.w)};
+        *(u32x2*)(a.y + ((xrow0 + tid) * a.Dm + d) * 4) = pk;
+      }
     }
     // (The next tile's first LDS writes of y and of (delta, s) come after barriers.)
   }
   __syncthreads();  // (with no tiles: the carried states' LDS writes above)
-  if (a.h_last && tid < S) {
+  if (a.h_last && tid < S && tid >= h_begin * kHalf && tid < h_end * kHalf) {
     const float4 hc = *(const float4*)(lds + kOffHC + tid * 16);
     *(float4*)(a.h_last + (bd * S + tid) * 4) = hc;
+  }
+}
+
+// The split walk's second launch: y = bf16(p0 + p1 + (D s, 0, 0, 0)) per (b, t, d), the
+// sum in the order the unsplit kernel makes it (half 0's partial, then half 1's, then
+// D s), so both forms give the same y bit for bit.
+__global__ __launch_bounds__(256) void fused_bc_combine_kernel(const float* __restrict__ ypart,
+                                                               const bf16_t* __restrict__ s,
+                                                               const float* __restrict__ dvec,
+                                                               __bf16* __restrict__ y,
+                                                               int64_t n, int64_t half_stride,
+                                                               int Dm) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const float4 p0 = *(const float4*)(ypart + e * 4);
+    const float4 p1 = *(const float4*)(ypart + (half_stride + e) * 4);
+    const float sv = io<bf16_t>::to_f32(s[e]);
+    const float dsk = dvec[e % Dm];
+    const u32x2 pk = {pk_bf16(fmaf(dsk, sv, p0.x + p1.x), p0.y + p1.y),
+                      pk_bf16(p0.z + p1.z, p0.w + p1.w)};
+    *(u32x2*)(y + e * 4) = pk;
   }
 }
 
@@ -489,13 +523,18 @@ int set_lds_limit(K kernel) {
 }
 }  // namespace
 
-extern "C" {
+namespace {
 
-int mqc_ssm_fused_bc_fwd(const void* x, const void* B_weight, const void* C_weight,
-                         const void* delta, const void* s, const float* lambda_alpha,
-                         const float* lambda_imag, const float* D, const void* h0, void* y,
-                         void* h_last, int64_t batch, int64_t seq_len, int64_t d_inner,
-                         int64_t d_state, float eps, int dtype, void* stream) {
+int64_t split_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_inner, int64_t d_state) {
+  if (batch <= 0 || seq_len <= 0 || d_inner <= 0 || d_state <= kHalf) return 0;
+  return 2 * batch * seq_len * d_inner * 4 * (int64_t)sizeof(float);
+}
+
+int fused_bc_run(const void* x, const void* B_weight, const void* C_weight, const void* delta,
+                 const void* s, const float* lambda_alpha, const float* lambda_imag,
+                 const float* D, const void* h0, void* y, void* h_last, int64_t batch,
+                 int64_t seq_len, int64_t d_inner, int64_t d_state, float eps, int dtype,
+                 bool split, void* workspace, int64_t workspace_bytes, void* stream) {
   if (batch < 0 || seq_len < 0 || d_inner < 0 || d_state < 0) return MQC_E_SHAPE;
   if (dtype != MQC_F32 && dtype != MQC_BF16 && dtype != MQC_F16) return MQC_E_DTYPE;
   if (dtype != MQC_BF16) return MQC_E_DTYPE;  // bf16 MFMAs only
@@ -509,9 +548,19 @@ int mqc_ssm_fused_bc_fwd(const void* x, const void* B_weight, const void* C_weig
       !aligned(delta, 2) || !aligned(s, 2) || (h0 && !aligned(h0, 16)) ||
       (h_last && !aligned(h_last, 16)))
     return MQC_E_ALIGN;
-  // 32-bit token and unit indices; one (b, d) per workgroup.
-  if (batch * d_inner > 0x7fffffffLL || batch * seq_len > (1LL << 30) || d_inner > (1 << 20))
+  // 32-bit token and unit indices; one (b, d) (or (b, d, half)) per workgroup.
+  if (batch * d_inner * kMaxHalves > 0x7fffffffLL || batch * seq_len > (1LL << 30) ||
+      d_inner > (1 << 20))
     return MQC_E_LIMIT;
+  // Split only where there are two halves and steps to walk; its partial sums go to
+  // the workspace.
+  split = split && split_workspace_bytes(batch, seq_len, d_inner, d_state) > 0;
+  if (split) {
+    if (!workspace) return MQC_E_NULL;
+    if (!aligned(workspace, 16)) return MQC_E_ALIGN;
+    if (workspace_bytes < split_workspace_bytes(batch, seq_len, d_inner, d_state))
+      return MQC_E_SPACE;
+  }
   // Each (b, d) reads h0 and writes h_last for its own states only, after its walk:
   // h_last may be h0, but not a shifted alias of it.
   if (partial_overlap(h0, h_last, batch * d_inner * d_state * 4 * (int64_t)sizeof(float)))
@@ -534,8 +583,11 @@ int mqc_ssm_fused_bc_fwd(const void* x, const void* B_weight, const void* C_weig
   a.delta = (const bf16_t*)delta; a.s = (const bf16_t*)s;
   a.lam_alpha = lambda_alpha; a.lam_imag = lambda_imag; a.dvec = D;
   a.h0 = (const float*)h0; a.y = (__bf16*)y; a.h_last = (float*)h_last;
+  a.ypart = split ? (float*)workspace : nullptr;
   a.batch = (int)batch; a.T = (int)seq_len; a.Dm = (int)d_inner; a.S = (int)d_state; a.eps = eps;
-  const dim3 grid((unsigned)(batch * d_inner));
+  a.split = split ? 1 : 0;
+  const int64_t units = batch * d_inner * (split ? kMaxHalves : 1);
+  const dim3 grid((unsigned)units);
   hipStream_t st = (hipStream_t)stream;
   const bool full_t = seq_len % kT == 0, full_s = d_state % kHalf == 0;
   if (full_t && full_s)
@@ -546,7 +598,46 @@ int mqc_ssm_fused_bc_fwd(const void* x, const void* B_weight, const void* C_weig
     hipLaunchKernelGGL((fused_bc_ssm_kernel<false, true>), grid, dim3(kThreads), kLdsFused, st, a);
   else
     hipLaunchKernelGGL((fused_bc_ssm_kernel<false, false>), grid, dim3(kThreads), kLdsFused, st, a);
+  if (!split) return launch_status();
+  int status = launch_status();
+  if (status != MQC_OK) return status;
+  const int64_t n = batch * seq_len * d_inner;
+  const int64_t blocks = (n + 255) / 256 < 16384 ? (n + 255) / 256 : 16384;
+  hipLaunchKernelGGL(fused_bc_combine_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                     (const float*)workspace, (const bf16_t*)s, D, (__bf16*)y, n, n,
+                     (int)d_inner);
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+int mqc_ssm_fused_bc_fwd(const void* x, const void* B_weight, const void* C_weight,
+                         const void* delta, const void* s, const float* lambda_alpha,
+                         const float* lambda_imag, const float* D, const void* h0, void* y,
+                         void* h_last, int64_t batch, int64_t seq_len, int64_t d_inner,
+                         int64_t d_state, float eps, int dtype, void* stream) {
+  return fused_bc_run(x, B_weight, C_weight, delta, s, lambda_alpha, lambda_imag, D, h0, y,
+                      h_last, batch, seq_len, d_inner, d_state, eps, dtype, false, nullptr, 0,
+                      stream);
+}
+
+int64_t mqc_ssm_fused_bc_split_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_inner,
+                                               int64_t d_state) {
+  if (batch < 0 || seq_len < 0 || d_inner < 0 || d_state < 0) return MQC_E_SHAPE;
+  return split_workspace_bytes(batch, seq_len, d_inner, d_state);
+}
+
+int mqc_ssm_fused_bc_fwd_split(const void* x, const void* B_weight, const void* C_weight,
+                               const void* delta, const void* s, const float* lambda_alpha,
+                               const float* lambda_imag, const float* D, const void* h0,
+                               void* y, void* h_last, int64_t batch, int64_t seq_len,
+                               int64_t d_inner, int64_t d_state, float eps, int dtype,
+                               void* workspace, int64_t workspace_bytes, void* stream) {
+  return fused_bc_run(x, B_weight, C_weight, delta, s, lambda_alpha, lambda_imag, D, h0, y,
+                      h_last, batch, seq_len, d_inner, d_state, eps, dtype, true, workspace,
+                      workspace_bytes, stream);
 }
 
 }  // extern "C"

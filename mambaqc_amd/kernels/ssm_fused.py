@@ -483,6 +483,14 @@ def ssm_forward_front_dl(dt_raw: torch.Tensor, g_raw: torch.Tensor, x: torch.Ten
 
 # --- B/C projections fused with the walk (inference) ---------------------------
 
+# Batches up to this size run the fused walk with each half of the states in a
+# workgroup of its own (mqc_ssm_fused_bc_fwd_split). A workgroup streams its d's weight
+# rows once per 256-token tile; the workgroups of a d's batches share those reads in L2,
+# a single sequence's do not, and its resident d's then want more weight rows than the
+# Infinity Cache holds. Config-3 width, one call: d_state 64 at batch 1, T2048 5.26 ms in
+# one workgroup per d, against 2 x 2.21 ms for two halves' worth of work (d_state 32).
+FUSED_BC_SPLIT_MAX_BATCH = 1
+
 def fused_bc_eligible(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torch.Tensor,
                       d_state: int) -> bool:
     """Whether ssm_forward_fused_bc takes these operands: bf16 x [batch, T, d_inner]
@@ -499,7 +507,8 @@ def fused_bc_eligible(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torch.T
 def ssm_forward_fused_bc(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torch.Tensor,
                          delta: torch.Tensor, s: torch.Tensor, lambda_alpha: torch.Tensor,
                          lambda_imag: torch.Tensor, D: torch.Tensor, eps: float = 1e-6,
-                         h0: torch.Tensor | None = None, return_state: bool = False):
+                         h0: torch.Tensor | None = None, return_state: bool = False,
+                         split: bool | None = None):
     """The block's B/C projections and its SSM in one HIP launch (inference, bf16).
 
     B = x B_weight^T and C = x C_weight^T, as [batch, seq_len, d_inner, d_state, 4]
@@ -511,6 +520,9 @@ def ssm_forward_fused_bc(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torc
     [d_inner * d_state * 4, d_inner] bf16; delta, s, the Lambda parameters, D and h0
     as in ssm_forward_fused_dl. Returns y [batch, seq_len, d_inner, 4] bf16 (and the
     final fp32 state if return_state). Inference only (no autograd).
+    split: run each half of the states (32) in a workgroup of its own, with a
+    workspace for the halves' partial sums and a second launch adding them (the
+    same y bit for bit); None splits batches of at most FUSED_BC_SPLIT_MAX_BATCH.
     """
     batch, T, d_inner = x.shape
     d_state = lambda_alpha.shape[-1] if lambda_alpha.dim() == 2 else 0
@@ -537,9 +549,19 @@ def ssm_forward_fused_bc(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torc
     y = torch.empty(batch, T, d_inner, 4, device=x.device, dtype=bf)
     h_last = (torch.empty(batch, d_inner, d_state, 4, device=x.device, dtype=torch.float32)
               if return_state else None)
-    nat.call("mqc_ssm_fused_bc_fwd", xc, xc.data_ptr(), wb.data_ptr(), wc.data_ptr(),
-             dl.data_ptr(), sv.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(),
-             nat.ptr(h0c), y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state,
-             float(eps), nat.BF16, nat.stream_of(xc))
+    args = (dl.data_ptr(), sv.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(),
+            nat.ptr(h0c), y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state,
+            float(eps), nat.BF16)
+    if split is None:
+        split = batch <= FUSED_BC_SPLIT_MAX_BATCH
+    ws_bytes = (nat.load().mqc_ssm_fused_bc_split_workspace_bytes(batch, T, d_inner, d_state)
+                if split else 0)
+    if ws_bytes > 0:
+        ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+        nat.call("mqc_ssm_fused_bc_fwd_split", xc, xc.data_ptr(), wb.data_ptr(), wc.data_ptr(),
+                 *args, ws.data_ptr(), ws_bytes, nat.stream_of(xc))
+    else:
+        nat.call("mqc_ssm_fused_bc_fwd", xc, xc.data_ptr(), wb.data_ptr(), wc.data_ptr(),
+                 *args, nat.stream_of(xc))
     return (y, h_last) if return_state else y
 

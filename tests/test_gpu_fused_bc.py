@@ -160,10 +160,9 @@ def test_fused_bc_rejects_what_it_cannot_run():
 
 def test_block_forward_fused_bc_path():
     """QuaternionMamba2Block inference in bf16 takes the fused path from
-    FUSED_BC_MIN_SEQ tokens and FUSED_BC_MIN_BATCH sequences on: its output against
-    the same block with fusion off and against the CPU oracle of the block (fp32 on
-    the same bf16 weights), and a sequence fed in two pieces through
-    forward_with_state against the whole."""
+    FUSED_BC_MIN_SEQ tokens on: its output against the same block with fusion off
+    and against the CPU oracle of the block (fp32 on the same bf16 weights), a
+    sequence fed in two pieces through forward_with_state against the whole."""
     import mambaqc_amd
     from mambaqc_amd import block as blockmod
 
@@ -173,11 +172,12 @@ def test_block_forward_fused_bc_path():
     x = torch.randn(2, 300, 64, generator=g, device=DEV).to(BF)
     assert x.shape[1] >= blockmod.FUSED_BC_MIN_SEQ and blk._use_fused_bc(
         torch.empty(2, 300, blk.d_inner, device=DEV, dtype=BF))
-    # A batch of one keeps the unfused path unless fusion is forced.
-    one = torch.empty(1, 300, blk.d_inner, device=DEV, dtype=BF)
-    assert blockmod.FUSED_BC_MIN_BATCH == 2 and not blk._use_fused_bc(one)
+    # A batch of one fuses too (split halves); short sequences do not unless forced.
+    assert blk._use_fused_bc(torch.empty(1, 300, blk.d_inner, device=DEV, dtype=BF))
+    short = torch.empty(2, blockmod.FUSED_BC_MIN_SEQ - 1, blk.d_inner, device=DEV, dtype=BF)
+    assert not blk._use_fused_bc(short)
     blk.fuse_bc = True
-    assert blk._use_fused_bc(one)
+    assert blk._use_fused_bc(short)
     blk.fuse_bc = None
     with torch.no_grad():
         got = blk(x)
@@ -191,3 +191,86 @@ def test_block_forward_fused_bc_path():
     want = oracle.block_forward_reference(sd, x.float().cpu(), d_state=16)
     assert_close(got, want, 2e-2, "block fused vs oracle")
     assert_close(torch.cat([out1, out2], 1), got, 2e-2, "fused block in pieces vs whole")
+
+
+@pytest.mark.parametrize("shape,with_h0", [
+    ((1, 300, 128, 64), False),   # ragged last tile, two full halves
+    ((1, 600, 64, 48), True),     # the second half ragged (16 states)
+    ((2, 512, 128, 64), True),    # batch 2, state carried across tiles
+    ((1, 256, 64, 32), False),    # one half: the split call is the one-launch form
+])
+def test_fused_bc_split_equals_one_launch(shape, with_h0):
+    """Each half of the states in a workgroup of its own, partial sums added by a
+    second launch (mqc_ssm_fused_bc_fwd_split): y and h_last equal the one-launch
+    form bit for bit, and the oracle to bf16 tolerance."""
+    b, T, d, k = shape
+    print(f"fused_bc split {shape} h0={with_h0}", flush=True)
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=11 + sum(shape))
+    h0 = h0 if with_h0 else None
+    with torch.no_grad():
+        y1, h1 = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0,
+                                        return_state=True, split=False)
+        y2, h2 = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0,
+                                        return_state=True, split=True)
+    assert torch.equal(y1, y2) and torch.equal(h1, h2)
+    want_y, want_h = _oracle(x, wb, wc, delta, s, la, li, D, h0, slice(None))
+    assert_close(y2, want_y, 2e-2, f"split y {shape}")
+    assert_close(h2, want_h, 2e-2, f"split h_last {shape}")
+
+
+def test_fused_bc_split_through_c_abi():
+    """The split entry point through the C ABI: h_last may be h0 (each half's
+    workgroup reads and writes only its own states), a short workspace is refused
+    before any launch, and the default of ssm_forward_fused_bc splits a batch of one."""
+    from mambaqc_amd.kernels import ssm_fused
+
+    b, T, d, k = 1, 300, 64, 64
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=21)
+    with torch.no_grad():
+        y_ref, h_ref = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0,
+                                              return_state=True, split=False)
+    assert ssm_fused.FUSED_BC_SPLIT_MAX_BATCH >= 1
+    lib = nat.load()
+    need = lib.mqc_ssm_fused_bc_split_workspace_bytes(b, T, d, k)
+    assert need == 2 * b * T * d * 16
+    ws = torch.empty(need, device=DEV, dtype=torch.uint8)
+    h = h0.clone()
+    y = torch.empty_like(y_ref)
+    stream = torch.cuda.current_stream().cuda_stream
+    P = [x.data_ptr(), wb.data_ptr(), wc.data_ptr(), delta.data_ptr(), s.data_ptr(),
+         la.data_ptr(), li.data_ptr(), D.data_ptr(), h.data_ptr(), y.data_ptr(), h.data_ptr(),
+         b, T, d, k, 1e-6, nat.BF16]
+    assert lib.mqc_ssm_fused_bc_fwd_split(*P, ws.data_ptr(), need - 16, stream) == -6
+    assert lib.mqc_ssm_fused_bc_fwd_split(*P, None, need, stream) == -1
+    assert torch.equal(h, h0)
+    st = lib.mqc_ssm_fused_bc_fwd_split(*P, ws.data_ptr(), need, stream)
+    assert st == 0, nat.status_string(st)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref) and torch.equal(h, h_ref)
+    with torch.no_grad():
+        y_def = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0)
+    assert torch.equal(y_def, y_ref)
+
+
+def test_block_batch_of_one_takes_split_fused_path():
+    """A batch of one with two halves of states (d_state 64) runs the split fused
+    kernel inside the block: against the same block unfused, its row of a batch of
+    two (one workgroup per d) and the CPU oracle of the block."""
+    import mambaqc_amd
+
+    torch.manual_seed(4)
+    blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=64).to(DEV, BF).eval()
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = torch.randn(2, 280, 64, generator=g, device=DEV).to(BF)
+    with torch.no_grad():
+        one = blk(x[:1])
+        both = blk(x)
+        blk.fuse_bc = False
+        one_unfused = blk(x[:1])
+        blk.fuse_bc = None
+    # (torch's GEMMs around the SSM may tile 280 and 560 rows differently.)
+    assert_close(one, both[:1], 2e-2, "split fused block vs its row of a batch of two")
+    assert_close(one, one_unfused, 2e-2, "split fused block vs unfused, batch of one")
+    sd = {k: v.detach().float().cpu() for k, v in blk.state_dict().items()}
+    want = oracle.block_forward_reference(sd, x[:1].float().cpu(), d_state=64)
+    assert_close(one, want, 2e-2, "split fused block vs oracle")

@@ -29,7 +29,7 @@ def declared_symbols():
 
 def test_header_declares_the_api():
     names = declared_symbols()
-    assert len(names) == 35, names
+    assert len(names) == 37, names
     assert set(nat.SIGNATURES) | set(nat.SIGNATURES_I64) <= set(names)
 
 
@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     lib = nat.load()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mqc_abi_version() == nat.ABI_VERSION == 6
+    assert lib.mqc_abi_version() == nat.ABI_VERSION == 7
 
 
 def test_status_strings():
@@ -250,6 +250,23 @@ def test_whole_walks_refuse_shifted_state_alias_without_gpu():
     #  dtype, stream)
     assert lib.mqc_ssm_fused_bc_fwd(*[FAKE] * 8, H, FAKE, H_part, b, T, d, k, 1e-6, 1,
                                     None) == -7
+
+
+def test_fused_bc_split_workspace_without_gpu():
+    """The split fused walk's workspace: two fp32 partial sums of y when there are
+    two halves of states and steps to walk, none otherwise; a missing, short or
+    misaligned workspace is refused before any HIP call."""
+    lib = nat.load()
+    assert lib.mqc_ssm_fused_bc_split_workspace_bytes(1, 2048, 1536, 64) == 2 * 2048 * 1536 * 16
+    assert lib.mqc_ssm_fused_bc_split_workspace_bytes(3, 7, 64, 34) == 2 * 3 * 7 * 64 * 16
+    assert lib.mqc_ssm_fused_bc_split_workspace_bytes(1, 2048, 1536, 32) == 0
+    assert lib.mqc_ssm_fused_bc_split_workspace_bytes(1, 0, 1536, 64) == 0
+    assert lib.mqc_ssm_fused_bc_split_workspace_bytes(-1, 2, 64, 64) == -2
+    need = lib.mqc_ssm_fused_bc_split_workspace_bytes(1, 16, 64, 64)
+    P = [FAKE] * 8 + [None, FAKE, None, 1, 16, 64, 64, 1e-6, 1]
+    assert lib.mqc_ssm_fused_bc_fwd_split(*P, None, need, None) == -1
+    assert lib.mqc_ssm_fused_bc_fwd_split(*P, FAKE, need - 1, None) == -6
+    assert lib.mqc_ssm_fused_bc_fwd_split(*P, ctypes.c_void_p(4096 + 8), need, None) == -4
 
 
 def test_fused_bc_validation_without_gpu():
