@@ -340,7 +340,7 @@ def run_full(args):
             lambda: mqc_gemm(xa, wb, gemm_out), 5)
         del gemm_out, xa
         # The block's inference paths on the same block and input, interleaved
-        # (median over rounds): the default (B/C projections fused into the SSM
+        # (median over 6 rounds): the default (B/C projections fused into the SSM
         # kernel, output step as out_proj then the gate kernel), B/C unfused
         # (hipBLASLt GEMMs, then the SSM kernel), and the output step fused.
         variants = {
@@ -349,9 +349,12 @@ def run_full(args):
             "block forward, output step fused (mqc_out_proj_gate_fwd)": (None, True),
         }
         ab = {k: [] for k in variants}
-        for _ in range(4):
-            for name, (fbc, fout) in variants.items():
-                blk.fuse_bc, blk.fuse_out = fbc, fout
+        names = list(variants)
+        for r in range(6):
+            # The order rotates from round to round, so no variant always follows
+            # the same one.
+            for name in names[r % 3:] + names[:r % 3]:
+                blk.fuse_bc, blk.fuse_out = variants[name]
                 blk(x)
                 ab[name].append(event_time_ms(lambda: blk(x), 3))
         blk.fuse_bc = blk.fuse_out = None
@@ -480,29 +483,38 @@ LONG_TRAIN_T = 65536
 
 def long_context_timing(blk):
     """The benchmark's block (config-3 width, bf16) on one sequence of LONG_T
-    tokens. Whole B and C would take 2 x 206 GB; the inference forward slices
-    them (BC_WHOLE_MAX_BYTES), 8 d's per slice of 2 GiB, each slice's SSM cut
-    into time chunks."""
+    tokens. Whole B and C would take 2 x 206 GB. The block's inference path runs
+    the fused B/C kernel in its split form (B and C never stored; two fp32 partial
+    sums of y in a workspace); beside it, the d-sliced path (fuse_bc off: 8 d's per
+    B/C slice of 2 GiB, each slice's SSM cut into time chunks)."""
     import torch
     from mambaqc_amd import block as bm
 
     g = torch.Generator(device="cuda").manual_seed(1)
     x = torch.randn(1, LONG_T, DM, generator=g, device="cuda").to(torch.bfloat16)
     width = bm.bc_slice_width(1, LONG_T, DI, DS, 2)
-    torch.cuda.reset_peak_memory_stats()
-    base_mem = torch.cuda.memory_allocated()
-    with torch.inference_mode():
-        blk(x)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        reps = 2
-        for _ in range(reps):
+
+    def timed():
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        base_mem = torch.cuda.memory_allocated()
+        with torch.inference_mode():
             blk(x)
-        torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / reps
-    peak = torch.cuda.max_memory_allocated() - base_mem
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(2):
+                blk(x)
+            torch.cuda.synchronize()
+        return ((time.perf_counter() - t0) * 1e3 / 2,
+                (torch.cuda.max_memory_allocated() - base_mem) / 2**30)
+
+    ms, peak = timed()
+    blk.fuse_bc = False
+    sliced_ms, sliced_peak = timed()
+    blk.fuse_bc = None
     log(f"long context: B1 T{LONG_T} block forward {ms:.1f} ms ({LONG_T / ms * 1e3:.0f} tokens/s), "
-        f"{width} d's per B/C slice, peak {peak / 2**30:.1f} GiB beyond the inputs")
+        f"fused B/C (split), peak {peak:.1f} GiB beyond the inputs; d-sliced B/C "
+        f"({width} d's per slice) {sliced_ms:.1f} ms, peak {sliced_peak:.1f} GiB")
     del x
     torch.cuda.empty_cache()
     # Training at LONG_TRAIN_T tokens: slices recomputed in the backward, the
@@ -530,10 +542,15 @@ def long_context_timing(blk):
     del xt
     torch.cuda.empty_cache()
     return {"workload": f"QuaternionMamba2Block forward (config-3 width, bf16), batch 1, "
-                        f"seq_len {LONG_T}, B/C projections in d-slices",
+                        f"seq_len {LONG_T}, B/C projections fused into the SSM kernel "
+                        f"(split halves)",
             "ms_per_step": round(ms, 2), "tokens_per_s": round(LONG_T / ms * 1e3, 1),
-            "bc_slice_d": width, "whole_bc_bytes": 2 * LONG_T * DI * DS * 4 * 2,
-            "peak_alloc_GiB": round(peak / 2**30, 2),
+            "whole_bc_bytes": 2 * LONG_T * DI * DS * 4 * 2,
+            "peak_alloc_GiB": round(peak, 2),
+            "sliced": {"workload": "fuse_bc off: B/C projections in d-slices, chunked walks",
+                       "ms_per_step": round(sliced_ms, 2),
+                       "tokens_per_s": round(LONG_T / sliced_ms * 1e3, 1),
+                       "bc_slice_d": width, "peak_alloc_GiB": round(sliced_peak, 2)},
             "train": {"workload": f"forward + backward, bf16, batch 1, seq_len {LONG_TRAIN_T}, "
                                   f"B/C in d-slices recomputed in the backward, chunked SSM "
                                   f"training walk and backward",
@@ -745,7 +762,7 @@ def run_kernel_loop(args):
             nbytes = sum(p.numel() * p.element_size() for p in lm.parameters())
         elif args.mode == "block_long":
             # The long-context line: the benchmark's block on one sequence of
-            # LONG_T tokens, B/C projections in d-slices.
+            # LONG_T tokens (its default path: the split fused B/C kernel).
             torch.manual_seed(0)
             with torch.inference_mode(False):
                 blk = make_block(torch.bfloat16)
