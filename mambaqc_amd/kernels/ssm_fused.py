@@ -490,6 +490,10 @@ def ssm_forward_front_dl(dt_raw: torch.Tensor, g_raw: torch.Tensor, x: torch.Ten
 # Infinity Cache holds. Config-3 width, one call: d_state 64 at batch 1, T2048 5.26 ms in
 # one workgroup per d, against 2 x 2.21 ms for two halves' worth of work (d_state 32).
 FUSED_BC_SPLIT_MAX_BATCH = 1
+# The split form's workspace (two fp32 partial sums of y, 49 KiB per token at d_inner
+# 1536) stays under this many bytes: a longer sequence of one batch row is walked in
+# segments of time, the state carried from one to the next through h0 / h_last.
+FUSED_BC_SPLIT_WS_MAX = 4 << 30
 
 def fused_bc_eligible(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torch.Tensor,
                       d_state: int) -> bool:
@@ -549,19 +553,37 @@ def ssm_forward_fused_bc(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torc
     y = torch.empty(batch, T, d_inner, 4, device=x.device, dtype=bf)
     h_last = (torch.empty(batch, d_inner, d_state, 4, device=x.device, dtype=torch.float32)
               if return_state else None)
-    args = (dl.data_ptr(), sv.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(),
-            nat.ptr(h0c), y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state,
-            float(eps), nat.BF16)
     if split is None:
         split = batch <= FUSED_BC_SPLIT_MAX_BATCH
-    ws_bytes = (nat.load().mqc_ssm_fused_bc_split_workspace_bytes(batch, T, d_inner, d_state)
-                if split else 0)
-    if ws_bytes > 0:
-        ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
-        nat.call("mqc_ssm_fused_bc_fwd_split", xc, xc.data_ptr(), wb.data_ptr(), wc.data_ptr(),
-                 *args, ws.data_ptr(), ws_bytes, nat.stream_of(xc))
-    else:
+    lib = nat.load()
+    ws_bytes = lib.mqc_ssm_fused_bc_split_workspace_bytes(batch, T, d_inner, d_state) if split else 0
+    stream = nat.stream_of(xc)
+    if ws_bytes <= 0:
         nat.call("mqc_ssm_fused_bc_fwd", xc, xc.data_ptr(), wb.data_ptr(), wc.data_ptr(),
-                 *args, nat.stream_of(xc))
+                 dl.data_ptr(), sv.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(),
+                 nat.ptr(h0c), y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state,
+                 float(eps), nat.BF16, stream)
+        return (y, h_last) if return_state else y
+    # Split: one launch over the whole sequence, or (a batch of one whose workspace
+    # would pass FUSED_BC_SPLIT_WS_MAX) segments of whole 256-token tiles.
+    seg = T
+    if batch == 1 and ws_bytes > FUSED_BC_SPLIT_WS_MAX:
+        per_token = ws_bytes // T
+        seg = max(256, FUSED_BC_SPLIT_WS_MAX // per_token // 256 * 256)
+    if seg < T:
+        ws_bytes = lib.mqc_ssm_fused_bc_split_workspace_bytes(batch, seg, d_inner, d_state)
+    ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+    state = h_last
+    if seg < T and state is None:
+        state = torch.empty(batch, d_inner, d_state, 4, device=x.device, dtype=torch.float32)
+    for t0 in range(0, T, seg):
+        t1 = min(T, t0 + seg)
+        # (A batch of one: every time slice is contiguous.)
+        nat.call("mqc_ssm_fused_bc_fwd_split", xc, xc[:, t0:t1].data_ptr(), wb.data_ptr(),
+                 wc.data_ptr(), dl[:, t0:t1].data_ptr(), sv[:, t0:t1].data_ptr(),
+                 la.data_ptr(), li.data_ptr(), Dv.data_ptr(),
+                 nat.ptr(h0c) if t0 == 0 else state.data_ptr(), y[:, t0:t1].data_ptr(),
+                 nat.ptr(state), batch, t1 - t0, d_inner, d_state, float(eps), nat.BF16,
+                 ws.data_ptr(), ws_bytes, stream)
     return (y, h_last) if return_state else y
 

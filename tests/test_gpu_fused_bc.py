@@ -274,3 +274,22 @@ def test_block_batch_of_one_takes_split_fused_path():
     sd = {k: v.detach().float().cpu() for k, v in blk.state_dict().items()}
     want = oracle.block_forward_reference(sd, x[:1].float().cpu(), d_state=64)
     assert_close(one, want, 2e-2, "split fused block vs oracle")
+
+
+def test_fused_bc_split_in_time_segments(monkeypatch):
+    """A batch of one whose split workspace would pass FUSED_BC_SPLIT_WS_MAX is
+    walked in segments of whole 256-token tiles, the fp32 state carried through
+    h0 / h_last: the same y and final state as one launch, bit for bit."""
+    from mambaqc_amd.kernels import ssm_fused
+
+    b, T, d, k = 1, 700, 64, 64
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=31)
+    with torch.no_grad():
+        y1, h1 = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0,
+                                        return_state=True, split=False)
+        # 2 x d x 16 bytes of workspace per token: segments of 256, 256 and 188 tokens.
+        monkeypatch.setattr(ssm_fused, "FUSED_BC_SPLIT_WS_MAX", 2 * d * 16 * 300)
+        y2, h2 = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0,
+                                        return_state=True, split=True)
+        y3 = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0, split=True)
+    assert torch.equal(y1, y2) and torch.equal(h1, h2) and torch.equal(y1, y3)
