@@ -33,6 +33,13 @@
 //           LDS accumulator of the tile's y (summed over the halves);
 //   4. after the last half: y = accumulator + D s, rounded to bf16.
 // The state of each half is carried from tile to tile in LDS (fp32), from h0 to h_last.
+//
+// Split form (a batch of one): one workgroup per (b, d, half), launched d-major with the
+// halves adjacent. A d's workgroup streams its weight rows once per tile, and only the
+// batches of a d share those reads, so a single sequence's 256 resident d's would want
+// 384 MiB of weight rows, more than the Infinity Cache; a half's workgroup wants half of
+// that. Each writes its half's fp32 partial sum of the tile's y (step 4 without D s) to
+// the caller's workspace, and fused_bc_combine_kernel adds the halves and D s.
 #include <atomic>
 
 #include "mfma_tile.hpp"
@@ -278,8 +285,9 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
     return XRows<FULL_T>{a.x, (int64_t)b * a.T + ti * kT, tv, K};
   };
   // delta and s of time tile ti, one token per thread of the first 256 (zero past the
-  // sequence: q = 1 and no input, so padded steps leave the state as it is). Held in
-  // registers until the tile's first K loop has waited for them, then stored to LDS.
+  // sequence: no input; the walk takes q = 1 there, so padded steps leave the state as
+  // it is). Held in registers until the tile's first K loop has waited for them, then
+  // stored to LDS.
   float dl_t = 0.f, s_t = 0.f;
   auto load_ds = [&](int ti) {
     const int tv = FULL_T ? kT : (a.T - ti * kT < kT ? a.T - ti * kT : kT);
@@ -359,7 +367,14 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
           const u32x2 br = *(const u32x2*)(lds + t * kTokBytes + ((kx ^ j) << 3));
           const quat Bq{bf_lo(br[0]), bf_hi(br[0]), bf_lo(br[1]), bf_hi(br[1])};
           float c;
-          const quat qq = cayley_step_c(ds.x, ds.x * ds.x, L, a.eps, c);
+          quat qq = cayley_step_c(ds.x, ds.x * ds.x, L, a.eps, c);
+          if constexpr (!FULL_T) {
+            // Past the sequence q is the identity, not Cayley(0) = 1 / max(1, eps).
+            if ((int)t >= tv) {
+              qq = quat{1.f, 0.f, 0.f, 0.f};
+              c = 0.f;
+            }
+          }
           hh = state_step(qq, hh, ds.y, Bq);
           const float na = fmaf(qq.w, ca, -c * cb * vv);
           cb = fmaf(qq.w, cb, c * ca);

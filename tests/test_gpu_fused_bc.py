@@ -49,7 +49,7 @@ def _bc_rounded(x, w, d_slice, k):
     return out.double().cpu().view(b, T, -1, k, 4)
 
 
-def _oracle(x, wb, wc, delta, s, la, li, D, h0, d_slice, b_slice=slice(None)):
+def _oracle(x, wb, wc, delta, s, la, li, D, h0, d_slice, b_slice=slice(None), eps=1e-6):
     k = la.shape[-1]
     xs = x[b_slice]
     Bq = _bc_rounded(xs, wb, d_slice, k)
@@ -57,7 +57,7 @@ def _oracle(x, wb, wc, delta, s, la, li, D, h0, d_slice, b_slice=slice(None)):
     up = lambda t: t.detach().double().cpu()
     return oracle.ssm_forward_dl_reference(
         up(delta[b_slice][:, :, d_slice]), up(s[b_slice][:, :, d_slice]), Bq, Cq,
-        up(la[d_slice]), up(li[d_slice]), up(D[d_slice]),
+        up(la[d_slice]), up(li[d_slice]), up(D[d_slice]), eps=eps,
         h0=None if h0 is None else up(h0[b_slice][:, d_slice]), return_state=True)
 
 
@@ -293,3 +293,18 @@ def test_fused_bc_split_in_time_segments(monkeypatch):
                                         return_state=True, split=True)
         y3 = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0, split=True)
     assert torch.equal(y1, y2) and torch.equal(h1, h2) and torch.equal(y1, y3)
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_fused_bc_eps_clamp(split):
+    """An eps large enough that the clamp max(N, eps) of the Cayley map engages on
+    the steps with small delta (N = 1 - delta a + delta^2 |Lambda|^2 / 4 >= 1 here,
+    eps 1.6): the fused walk, in both forms, against the oracle with the same eps."""
+    b, T, d, k = 1, 300, 64, 64
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=41)
+    with torch.no_grad():
+        y, h = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, eps=1.6, h0=h0,
+                                      return_state=True, split=split)
+    want_y, want_h = _oracle(x, wb, wc, delta, s, la, li, D, h0, slice(None), eps=1.6)
+    assert_close(y, want_y, 2e-2, "fused y, eps clamp")
+    assert_close(h, want_h, 2e-2, "fused h_last, eps clamp")
