@@ -1,7 +1,7 @@
 """Benchmark: QuaternionMamba2Block forward on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
-                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_train|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|fused_bc|bc_unfused|out_step|out_step_unfused|decode|decode_graph|block_long|train|copy]
+                    [--mode full|ssm|ssm_b1|ssm_b1_whole|ssm_train|ssm_bwd|cumprod|cayley|qln|gemm|gemm_hipblaslt|fused_bc|bc_unfused|out_step|out_step_unfused|out_step_block|decode|decode_graph|block_long|train|copy]
                     [--preset small|base|large]
 
 Workload (BASELINE configs[2]/[3] shape): one QuaternionMamba2Block forward,
@@ -836,6 +836,21 @@ def run_kernel_loop(args):
                 fn = lambda: out_proj_gate(xo, zo, yo, wo)
             else:
                 fn = lambda: out_gate(xo, zo, torch.nn.functional.linear(yo.view(B * T, -1), wo))
+            nbytes = 0
+        elif args.mode == "out_step_block":
+            # The output step inside the block, for a kernel trace: per step, four
+            # config-3 block forwards with the fused output step, then four unfused.
+            torch.manual_seed(0)
+            with torch.inference_mode(False):
+                blk = make_block(torch.bfloat16)
+            x = torch.randn(B, T, DM, generator=g, device="cuda").to(torch.bfloat16)
+
+            def fn():
+                for fo in (True, False):
+                    blk.fuse_out = fo
+                    for _ in range(4):
+                        blk(x)
+                blk.fuse_out = None
             nbytes = 0
         elif args.mode == "copy":
             src = torch.empty(1 << 28, device="cuda")  # 1 GiB
