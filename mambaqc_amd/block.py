@@ -522,7 +522,7 @@ class QuaternionMamba2Block(nn.Module):
     def _use_fused_bc(self, x: torch.Tensor) -> bool:
         """Whether this inference forward runs the B/C projections fused into the
         SSM kernel (fuse_bc; the class docstring)."""
-        if self.fuse_bc is False or nat.compiling() or (self.bc_slice_d or 0) > 0:
+        if self.fuse_bc is False or (self.bc_slice_d or 0) > 0:
             return False
         if self.B_proj.bias is not None or self.C_proj.bias is not None:
             return False

@@ -530,6 +530,10 @@ def ssm_forward_fused_bc(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torc
     """
     batch, T, d_inner = x.shape
     d_state = lambda_alpha.shape[-1] if lambda_alpha.dim() == 2 else 0
+    if nat.compiling():
+        y, h_last = torch.ops.mambaqc.ssm_forward_fused_bc(x, B_weight, C_weight, delta, s,
+                                                           lambda_alpha, lambda_imag, D, h0, eps)
+        return (y, h_last) if return_state else y
     assert delta.shape == (batch, T, d_inner) and s.shape == (batch, T, d_inner)
     assert lambda_alpha.shape == (d_inner, d_state)
     assert lambda_imag.shape == (d_inner, d_state, 3)

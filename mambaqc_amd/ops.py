@@ -165,6 +165,25 @@ def _(delta, s, B, C, lambda_alpha, lambda_imag, D, h0=None, eps=1e-6, chunk_len
     return B.new_empty(b, t, d, 4), B.new_empty(b, d, n, 4, dtype=torch.float32)
 
 
+@custom_op(f"{NS}::ssm_forward_fused_bc", mutates_args=())
+def ssm_forward_fused_bc(x: Tensor, B_weight: Tensor, C_weight: Tensor, delta: Tensor, s: Tensor,
+                         lambda_alpha: Tensor, lambda_imag: Tensor, D: Tensor,
+                         h0: Optional[Tensor] = None,
+                         eps: float = 1e-6) -> Tuple[Tensor, Tensor]:
+    """The B/C projections and the inference walk in one kernel (bf16):
+    (y [B, T, D, 4] bf16, h_last [B, D, S, 4] fp32). Inference only."""
+    with torch.no_grad():
+        return sf.ssm_forward_fused_bc(x, B_weight, C_weight, delta, s, lambda_alpha, lambda_imag,
+                                       D, eps=eps, h0=h0, return_state=True)
+
+
+@ssm_forward_fused_bc.register_fake
+def _(x, B_weight, C_weight, delta, s, lambda_alpha, lambda_imag, D, h0=None, eps=1e-6):
+    b, t, d = x.shape
+    return (x.new_empty(b, t, d, 4), x.new_empty(b, d, lambda_alpha.shape[-1], 4,
+                                                 dtype=torch.float32))
+
+
 @custom_op(f"{NS}::ssm_forward_dl_train", mutates_args=())
 def ssm_forward_dl_train(delta: Tensor, s: Tensor, B: Tensor, C: Tensor, lambda_alpha: Tensor,
                          lambda_imag: Tensor, D: Tensor, h0: Optional[Tensor] = None,

@@ -114,6 +114,18 @@ def test_opcheck():
     xz = torch.randn(2, 7, 12, generator=g, device=DEV, requires_grad=True)
     yr = torch.randn(2, 7, 6, generator=g, device=DEV, requires_grad=True)
     opcheck(mm.out_gate, (x, xz, yr))
+    # The fused B/C walk (bf16, inference only).
+    bf = torch.bfloat16
+    xb = torch.randn(1, 9, 64, generator=g, device=DEV).to(bf)
+    wb = (torch.randn(64 * 4 * 4, 64, generator=g, device=DEV) * 0.05).to(bf)
+    wc = (torch.randn(64 * 4 * 4, 64, generator=g, device=DEV) * 0.05).to(bf)
+    db = torch.nn.functional.softplus(torch.randn(1, 9, 64, generator=g, device=DEV)).to(bf)
+    sb = torch.randn(1, 9, 64, generator=g, device=DEV).to(bf)
+    lab = torch.randn(64, 4, generator=g, device=DEV) * 0.5 + 1
+    lib_ = torch.randn(64, 4, 3, generator=g, device=DEV) * 0.1
+    Db = torch.ones(64, device=DEV)
+    with torch.no_grad():
+        opcheck(mm.ssm_forward_fused_bc, (xb, wb, wc, db, sb, lab, lib_, Db, None, 1e-6))
 
 
 def _grads(out, inputs, seed=5):
@@ -272,3 +284,26 @@ def test_block_compiles_fullgraph_fp16_autocast():
     names = ["x"] + [n for n, _ in blk.named_parameters()]
     for n, a, b in zip(names, gc, ge):
         assert_close(a, b, 2e-2, f"compiled block grad {n} (fp16 autocast)")
+
+
+def test_block_compiles_fused_bc_inference():
+    """A compiled bf16 block in inference takes the fused B/C walk as the operator
+    torch.ops.mambaqc.ssm_forward_fused_bc (sequences of FUSED_BC_MIN_SEQ tokens and
+    more): its output against the eager block, which runs the same kernel, and
+    against the compiled block with fusion off."""
+    from mambaqc_amd.block import FUSED_BC_MIN_SEQ
+    from conftest import assert_close
+
+    torch.manual_seed(6)
+    blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=16).to(DEV, torch.bfloat16).eval()
+    x = torch.randn(2, FUSED_BC_MIN_SEQ + 44, 64, generator=_g(8), device=DEV).to(torch.bfloat16)
+    compiled = torch.compile(blk, backend="aot_eager", fullgraph=True)
+    with torch.no_grad():
+        want = blk(x)
+        got = compiled(x)
+        blk.fuse_bc = False
+        torch._dynamo.reset()
+        unfused = torch.compile(blk, backend="aot_eager", fullgraph=True)(x)
+        blk.fuse_bc = None
+    assert torch.equal(got, want)
+    assert_close(got, unfused, 2e-2, "compiled block, fused vs unfused B/C")
