@@ -118,6 +118,11 @@ def test_fused_bc_config3_full_size():
                    (3, slice(1534, 1536))):
         want, _ = _oracle(x, wb, wc, delta, s, la, li, D, None, ds, slice(b0, b0 + 1))
         assert_close(y[b0:b0 + 1, :, ds], want, 2e-2, f"C3 fused slice b={b0} d={ds}")
+    # Every lane at full size: y is linear in s (B and C do not depend on it), and
+    # doubling is exact in floating point, so 2 s gives 2 y bit for bit.
+    with torch.no_grad():
+        y_2s = K.ssm_forward_fused_bc(x, wb, wc, delta, (2 * s.float()).to(BF), la, li, D)
+    assert torch.equal(y_2s, (2 * y.float()).to(BF))
 
 
 def test_fused_bc_state_in_place_and_empty():
