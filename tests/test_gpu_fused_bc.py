@@ -203,6 +203,7 @@ def test_block_forward_fused_bc_path():
     ((1, 600, 64, 48), True),     # the second half ragged (16 states)
     ((2, 512, 128, 64), True),    # batch 2, state carried across tiles
     ((1, 256, 64, 32), False),    # one half: the split call is the one-launch form
+    ((1, 1, 64, 64), True),       # one token
 ])
 def test_fused_bc_split_equals_one_launch(shape, with_h0):
     """Each half of the states in a workgroup of its own, partial sums added by a
