@@ -572,8 +572,11 @@ def ssm_forward_fused_bc(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torc
     # would pass FUSED_BC_SPLIT_WS_MAX) segments of whole 256-token tiles.
     seg = T
     if batch == 1 and ws_bytes > FUSED_BC_SPLIT_WS_MAX:
+        # Equal segments (whole tiles) of at most the budget's tokens.
         per_token = ws_bytes // T
-        seg = max(256, FUSED_BC_SPLIT_WS_MAX // per_token // 256 * 256)
+        seg_max = max(256, FUSED_BC_SPLIT_WS_MAX // per_token // 256 * 256)
+        n_seg = -(-T // seg_max)
+        seg = -(-T // (n_seg * 256)) * 256
     if seg < T:
         ws_bytes = lib.mqc_ssm_fused_bc_split_workspace_bytes(batch, seg, d_inner, d_state)
     ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
