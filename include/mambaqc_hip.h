@@ -46,7 +46,8 @@ extern "C" {
 #define MQC_E_OVERLAP (-7)   /* an output overlaps an input that the launch still reads
                               * (the chunked SSM walks: h_last over h0, dh0 over
                               * dh_last; every SSM walk: h_last sharing bytes with h0
-                              * without being the same buffer) */
+                              * without being the same buffer; the fused output step:
+                              * out over y, W, bias, z or a shifted x) */
 
 /* Human-readable text for a status code (static storage, never NULL). */
 const char* mqc_status_string(int status);
@@ -248,6 +249,8 @@ int mqc_ssm_fused_bc_fwd_split(const void* x, const void* B_weight, const void* 
  * it, gated by z [rows, >= d_model] (row stride z_row_stride elements, read in place:
  * the gate half of in_proj's output) and added to the residual x [rows, d_model].
  * y, W, x, z, out 16-byte aligned; d_model a multiple of 8, k of 64, z_row_stride of 8.
+ * out may be x itself (an in-place residual); out sharing bytes with y, W, bias, z or
+ * with x without being x is refused (MQC_E_OVERLAP): other tiles still read them.
  * Replaces out_proj (QuaternionLinear._forward_quaternion_to_real,
  * mambaqc/layers/quaternion_linear.py:163-172) with the gate and residual of
  * mambaqc/models/quaternion_mamba2_block.py:157-164 (z[..., :d_model], as the

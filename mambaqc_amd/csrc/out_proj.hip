@@ -169,9 +169,19 @@ int mqc_out_proj_gate_fwd(const void* y, const void* W, const void* bias, const 
       !aligned(out, 16) || (bias && !aligned(bias, 2)))
     return MQC_E_ALIGN;
   // 32-bit tile and row arithmetic.
-  if (rows > (1LL << 30) || d_model > (1LL << 20) || k > (1LL << 20)) return MQC_E_LIMIT;
+  if (rows > (1LL << 30) || d_model > (1LL << 20) || k > (1LL << 20) ||
+      z_row_stride > (1LL << 32))
+    return MQC_E_LIMIT;
   const int64_t tiles = (rows + kOM - 1) / kOM * ((d_model + kON - 1) / kON);
   if (tiles > 0x7fffffffLL) return MQC_E_LIMIT;
+  // Tiles write out while other tiles still read y, W, bias and z. out may be x itself
+  // (each 16-byte piece of x is read and then written by one thread), not a shifted x.
+  const int64_t out_bytes = rows * d_model * 2;
+  if (overlaps(out, out_bytes, y, rows * k * 2) || overlaps(out, out_bytes, W, d_model * k * 2) ||
+      overlaps(out, out_bytes, bias, bias ? d_model * 2 : 0) ||
+      overlaps(out, out_bytes, z, ((rows - 1) * z_row_stride + d_model) * 2) ||
+      partial_overlap(out, x, out_bytes))
+    return MQC_E_OVERLAP;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;

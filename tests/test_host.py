@@ -252,6 +252,29 @@ def test_whole_walks_refuse_shifted_state_alias_without_gpu():
                                     None) == -7
 
 
+def test_out_proj_gate_refuses_overlap_without_gpu():
+    """The fused output step writes out tile by tile while other tiles still read
+    y, W, bias and z: out sharing bytes with any of them, or with x without being
+    x, is refused (MQC_E_OVERLAP) before any HIP call."""
+    lib = nat.load()
+    rows, dm, k, zs = 64, 72, 128, 144
+    Y = 1 << 24
+    W = Y + rows * k * 2 + 4096
+    X = W + dm * k * 2 + 4096
+    Z = X + rows * dm * 2 + 4096
+    O = Z + rows * zs * 2 + 4096
+    p = ctypes.c_void_p
+
+    def call(out, bias=None):
+        # (y, W, bias, x, z, z_row_stride, out, rows, d_model, k, dtype, stream)
+        return lib.mqc_out_proj_gate_fwd(p(Y), p(W), p(bias) if bias else None, p(X), p(Z),
+                                         zs, p(out), rows, dm, k, 1, None)
+
+    for out in (Y + 16, W + 16, Z + (rows - 1) * zs * 2, X + 16, X - 16):
+        assert call(out) == -7, hex(out)
+    assert call(O, bias=O + rows * dm * 2 - 2) == -7
+
+
 def test_fused_bc_split_workspace_without_gpu():
     """The split fused walk's workspace: two fp32 partial sums of y when there are
     two halves of states and steps to walk, none otherwise; a missing, short or
