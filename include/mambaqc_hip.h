@@ -5,6 +5,10 @@
  * Conventions shared by every entry point
  *   - All tensor arguments are device pointers to contiguous, row-major
  *     buffers owned by the caller. Nothing is allocated inside the library.
+ *   - Outputs share no bytes with inputs, except where an entry point names an
+ *     in-place form (such as h_last == h0 for a walk's state, out == x for the
+ *     output step); the overlaps a launch could race on are checked where its
+ *     comment says so and refused with MQC_E_OVERLAP.
  *   - A quaternion is four consecutive elements (w, x, y, z).
  *   - `dtype` selects the storage type of the tensors named in each comment:
  *     MQC_F32, MQC_BF16 or MQC_F16. Arithmetic is always fp32. Parameter
