@@ -760,12 +760,15 @@ def run_kernel_loop(args):
                     graph = DecodeGraph(lm, states)
                 fn = lambda: graph.step(tok)
             nbytes = sum(p.numel() * p.element_size() for p in lm.parameters())
-        elif args.mode == "block_long":
+        elif args.mode in ("block_long", "block_long_sliced"):
             # The long-context line: the benchmark's block on one sequence of
-            # LONG_T tokens (its default path: the split fused B/C kernel).
+            # LONG_T tokens, on its default path (the split fused B/C kernel) or,
+            # block_long_sliced, with fuse_bc off (B/C projections in d-slices).
             torch.manual_seed(0)
             with torch.inference_mode(False):
                 blk = make_block(torch.bfloat16)
+            if args.mode == "block_long_sliced":
+                blk.fuse_bc = False
             x = torch.randn(1, LONG_T, DM, generator=g, device="cuda").to(torch.bfloat16)
             fn = lambda: blk(x)
             nbytes = 0
