@@ -203,9 +203,10 @@ int64_t mqc_ssm_chunked_scratch_bytes(void);
 int mqc_ssm_noalloc_prepare(void);
 
 /* The block's B and C projections fused with its SSM (mqc_ssm_fused_fwd) in one
- * launch, bf16 only (dtype MQC_BF16): B = x . B_weight^T and C = x . C_weight^T,
- * viewed as [batch, seq_len, d_inner, d_state, 4], are computed 256 tokens at a time
- * by MFMA tiles in LDS, rounded to bf16 as the unfused projections store them, and
+ * launch, 16-bit storage (dtype MQC_BF16 or MQC_F16, for x, the weights, delta, s and
+ * y; MQC_F32 is refused): B = x . B_weight^T and C = x . C_weight^T, viewed as
+ * [batch, seq_len, d_inner, d_state, 4], are computed 256 tokens at a time by MFMA
+ * tiles in LDS, rounded to dtype as the unfused projections store them, and
  * walked there, so neither is ever written to memory. x: [batch, seq_len, d_inner]
  * (the projections' input, 16-byte aligned); B_weight, C_weight: [d_inner * d_state * 4,
  * d_inner] (nn.Linear layout, 16-byte aligned); delta, s: [batch, seq_len, d_inner];

@@ -85,7 +85,7 @@ SIGNATURES_I64 = {
     "mqc_ssm_fused_bc_split_workspace_bytes": [_i64, _i64, _i64, _i64],
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lock = threading.Lock()
 _lib = None

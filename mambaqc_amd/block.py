@@ -10,7 +10,7 @@ under the same seed, identical state_dict keys), and the same forward:
     delta = softplus(dt_raw); s = sigmoid(g_raw) * x_act    HIP: mqc_ssm_front_fwd
     B, C = B_proj(x_act), C_proj(x_act) as [B,T,D,S,4]      torch GEMMs (hipBLASLt)
     y = SSM(Cayley(delta * Lambda), B, s, C, D)             HIP: mqc_ssm_fused_fwd
-      (bf16 inference of whole sequences: both lines as one  HIP: mqc_ssm_fused_bc_fwd,
+      (16-bit inference of whole sequences: both lines as one HIP: mqc_ssm_fused_bc_fwd,
        kernel that never stores B or C)
     y = QuaternionLayerNorm(y)                              HIP: mqc_qln_fwd
     y_real = out_proj(y)                                    torch GEMM
@@ -190,7 +190,7 @@ def _rows_uniform(z: torch.Tensor) -> bool:
 BC_WHOLE_MAX_BYTES = 32 << 30
 BC_SLICE_BYTES = 2 << 30
 
-# Inference in bf16 from this many tokens per sequence on: the B/C projections and the
+# Inference in bf16 or fp16 from this many tokens per sequence on: the B/C projections and the
 # SSM run as one kernel (mqc_ssm_fused_bc_fwd), B and C computed in 256-token tiles on
 # chip and never stored. Shorter sequences (a decode step, short prompts) would fill one
 # tile with a few tokens and keep the separate GEMMs. A batch of one runs the kernel with
@@ -387,8 +387,8 @@ class QuaternionMamba2Block(nn.Module):
 
     fuse_bc (attribute): None runs inference (no autograd) with the B/C
     projections fused into the SSM kernel (ssm_forward_fused_bc) where that
-    kernel applies (bf16, bias-free projections, d_inner a multiple of 64, even
-    d_state <= 64) and sequences have at least FUSED_BC_MIN_SEQ tokens; True
+    kernel applies (bf16 or fp16 without autocast, bias-free projections, d_inner
+    a multiple of 64, even d_state <= 64) and sequences have at least FUSED_BC_MIN_SEQ tokens; True
     also for shorter ones; False never. A forced bc_slice_d takes precedence.
 
     fuse_out (attribute): True runs the output step of bf16 inference (out_proj,

@@ -432,7 +432,7 @@ const char* mqc_status_string(int status) {
   }
 }
 
-int mqc_abi_version(void) { return 7; }
+int mqc_abi_version(void) { return 8; }
 
 int mqc_quaternion_multiply(const void* p, const void* q, void* out, int64_t n_quat, int dtype,
                             void* stream) {

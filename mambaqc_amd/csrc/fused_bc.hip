@@ -1,5 +1,6 @@
-// The block's B/C projections fused with its SSM walk (bf16): B and C are
-// computed tile by tile in LDS and walked there, so they never reach HBM.
+// The block's B/C projections fused with its SSM walk (bf16 or fp16 storage, fp32
+// accumulation): B and C are computed tile by tile in LDS and walked there, so they never
+// reach HBM.
 //
 //   B = x . W_B^T, C = x . W_C^T     (F.linear, mambaqc/layers/quaternion_linear.py:145-161,
 //                                     called at models/quaternion_mamba2_block.py:186-191),
@@ -18,8 +19,8 @@
 // states (32 states: 128 rows of W_B and the same 128 rows of W_C):
 //   1. GEMM: the 256 x 256 MFMA tile of mfma_tile.hpp, x[b, t0 : t0 + 256, :] against the
 //      half's 256 weight rows (B's 128, then C's 128), K = d_inner;
-//   2. the tile rounded to bf16 (the projections' storage dtype, so the walk sees the
-//      values the unfused path stores) into LDS over the GEMM's stages, as one 16-byte
+//   2. the tile rounded to the storage dtype (what the projections store, so the walk
+//      sees the values the unfused path stores) into LDS over the GEMM's stages, as one 16-byte
 //      cell (B quaternion, C quaternion) per (token, state);
 //   3. the walk over the tile's 256 tokens for the half's 32 states, by all 8 waves: the
 //      tokens in 16 chunks of 16, lane (state k, chunk c);
@@ -31,7 +32,7 @@
 //        c. each chunk again from its start state, with y's terms C (x) h, summed over the
 //           32 states by a reduce-scatter across the lanes of a half-wave, into an fp32
 //           LDS accumulator of the tile's y (summed over the halves);
-//   4. after the last half: y = accumulator + D s, rounded to bf16.
+//   4. after the last half: y = accumulator + D s, rounded to the storage dtype.
 // The state of each half is carried from tile to tile in LDS (fp32), from h0 to h_last.
 //
 // Split form (a batch of one): one workgroup per (b, d, half), launched d-major with the
@@ -54,7 +55,7 @@ constexpr int kHalf = 32;                 // states per half
 constexpr int kMaxHalves = 2;             // d_state <= 64
 constexpr int kNChunk = 16;               // chunks per tile
 constexpr int kChunkLen = kT / kNChunk;   // 16 tokens
-constexpr int kCellBytes = 8;             // one bf16 quaternion of one (token, state)
+constexpr int kCellBytes = 8;             // one 16-bit quaternion of one (token, state)
 constexpr int kTokBytes = kHalf * kCellBytes;  // 256 bytes per token in the B or the C tile
 constexpr int kOffC = kT * kTokBytes;          // the C tile after the B tile (64 KiB each)
 // LDS layout (bytes): the GEMM's two stages, reused for the B/C tile, then the walk's own.
@@ -72,17 +73,18 @@ static_assert(2 * kT * kTokBytes == kStagesBytes && kOffC == kStageBytes,
               "the B and C tiles are the GEMM's two stages");
 static_assert(kLdsFused <= 160 * 1024, "gfx950 LDS");
 
+// 16-bit tensors (bf16 or fp16, the kernel's T) as raw element bits.
 struct FusedArgs {
-  const __bf16* x;     // [batch, T, K] (K = d_inner)
-  const __bf16* wb;    // [d_inner * S * 4, K]
-  const __bf16* wc;
-  const bf16_t* delta;  // [batch, T, d_inner]
-  const bf16_t* s;
+  const uint16_t* x;   // [batch, T, K] (K = d_inner)
+  const uint16_t* wb;  // [d_inner * S * 4, K]
+  const uint16_t* wc;
+  const uint16_t* delta;  // [batch, T, d_inner]
+  const uint16_t* s;
   const float* lam_alpha;  // [d_inner, S]
   const float* lam_imag;   // [d_inner, S, 3]
   const float* dvec;       // [d_inner]
   const float* h0;         // [batch, d_inner, S, 4] or null
-  __bf16* y;               // [batch, T, d_inner, 4]
+  uint16_t* y;             // [batch, T, d_inner, 4]
   float* h_last;           // [batch, d_inner, S, 4] or null
   float* ypart;            // split: y's partial sums [halves, batch, T, d_inner, 4]
   int batch, T, Dm, S;
@@ -100,8 +102,8 @@ struct FusedArgs {
 // whole pairs of states, d_state being even); X rows the tile's tv tokens (rows past
 // the sequence read its last token).
 struct WRows {
-  const __bf16* wb;
-  const __bf16* wc;
+  const uint16_t* wb;
+  const uint16_t* wc;
   int64_t row0;
   int hs4, K;
   __device__ const void* operator()(int g, int k0, int i, uint32_t& voff,
@@ -114,7 +116,7 @@ struct WRows {
 };
 template <bool FULL_T>
 struct XRows {
-  const __bf16* x;
+  const uint16_t* x;
   int64_t row0;
   int tv, K;
   __device__ const void* operator()(int g, int k0, int i, uint32_t& voff,
@@ -140,8 +142,17 @@ __device__ inline V opaque(V v) {
   return v;
 }
 
-__device__ inline float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ inline float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+// The two 16-bit elements of a 32-bit word (low half first) in fp32.
+template <typename T>
+__device__ inline float lo16(uint32_t w) {
+  if constexpr (std::is_same<T, bf16_t>::value) return __uint_as_float(w << 16);
+  else return io<T>::bits_to_f32(w & 0xffffu);
+}
+template <typename T>
+__device__ inline float hi16(uint32_t w) {
+  if constexpr (std::is_same<T, bf16_t>::value) return __uint_as_float(w & 0xffff0000u);
+  else return io<T>::bits_to_f32(w >> 16);
+}
 
 // Exchange x of the odd 16-lane rows with y of the even rows (v_permlane16_swap_b32):
 // afterwards even-row lanes hold (own x, the odd neighbour's x) and odd-row lanes
@@ -222,10 +233,12 @@ __device__ inline void reduce_scatter32(float (&o)[64], int lane, float& r0, flo
   r1 = r2[1];
 }
 
-// FULL_T: T is a multiple of 256 (no ragged last tile). FULL_S: d_state is a multiple of
-// 32 (every half full).
-template <bool FULL_T, bool FULL_S>
+// T: the 16-bit storage type (bf16_t or f16_t), whose MFMAs the GEMM runs. FULL_T: the
+// sequence length is a multiple of 256 (no ragged last tile). FULL_S: d_state is a
+// multiple of 32 (every half full).
+template <typename T, bool FULL_T, bool FULL_S>
 __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
+  using E = typename std::conditional<std::is_same<T, bf16_t>::value, __bf16, _Float16>::type;
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -295,8 +308,8 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
     s_t = 0.f;
     if (tid < kT && tid < tv) {
       const int64_t e = ((int64_t)b * a.T + ti * kT + tid) * a.Dm + d;
-      dl_t = io<bf16_t>::to_f32(a.delta[e]);
-      s_t = io<bf16_t>::to_f32(a.s[e]);
+      dl_t = io<T>::bits_to_f32(a.delta[e]);
+      s_t = io<T>::bits_to_f32(a.s[e]);
     }
   };
   if (n_tiles > 0) load_ds(0);
@@ -312,10 +325,10 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       for (int i = 0; i < kWB; ++i)
 #pragma unroll
         for (int j = 0; j < kXB; ++j) acc[i][j] = (floatx4){};
-      tile_kloop(K, lds, acc, wrows(h), xrows(ti));
+      tile_kloop<E>(K, lds, acc, wrows(h), xrows(ti));
       if (h == h_begin && tid < kT) *(float2*)(lds + kOffDS + tid * 8) = float2{dl_t, s_t};
 
-      // ---- 2. The tile, rounded to bf16, over the stages (every wave is past its last
+      // ---- 2. The tile, rounded to T, over the stages (every wave is past its last
       // fragment read at the barrier).
       wait_lgkm0();
       __builtin_amdgcn_s_barrier();
@@ -331,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
           for (int mb = 0; mb < kXB; ++mb) {
             const uint32_t cst = (uint32_t)(nb * 4);
             const floatx4& v = acc[nb][mb];
-            const u32x2 pk = {pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])};
+            const u32x2 pk = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
             *(u32x2*)(lds + base + mb * 16 * kTokBytes + ((x0 ^ cst) << 3)) = pk;
           }
       }
@@ -365,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
           const uint32_t t = tb + j;
           const float2 ds = *(const float2*)(lds + kOffDS + t * 8);
           const u32x2 br = *(const u32x2*)(lds + t * kTokBytes + ((kx ^ j) << 3));
-          const quat Bq{bf_lo(br[0]), bf_hi(br[0]), bf_lo(br[1]), bf_hi(br[1])};
+          const quat Bq{lo16<T>(br[0]), hi16<T>(br[0]), lo16<T>(br[1]), hi16<T>(br[1])};
           float c;
           quat qq = cayley_step_c(ds.x, ds.x * ds.x, L, a.eps, c);
           if constexpr (!FULL_T) {
@@ -451,7 +464,7 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
         for (int j = 0; j < kChunkLen; ++j) {
           const uint32_t t = tb + j;
           const u32x2 r = *(const u32x2*)(lds + kOffC + t * kTokBytes + ((kx ^ j) << 3));
-          const quat Cq{bf_lo(r[0]), bf_hi(r[0]), bf_lo(r[1]), bf_hi(r[1])};
+          const quat Cq{lo16<T>(r[0]), hi16<T>(r[0]), lo16<T>(r[1]), hi16<T>(r[1])};
           const quat hh{fmaf(pa[j], hs0.w, fmaf(pb[j], vh.w, hl[j].w)),
                         fmaf(pa[j], hs0.x, fmaf(pb[j], vh.x, hl[j].x)),
                         fmaf(pa[j], hs0.y, fmaf(pb[j], vh.y, hl[j].y)),
@@ -488,7 +501,7 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
       } else {
         const float dsk = a.dvec[d];
         const float sv = (*(const float2*)(lds + kOffDS + tid * 8)).y;
-        const u32x2 pk = {pk_bf16(fmaf(dsk, sv, yv.x), yv.y), pk_bf16(yv.z, yv.w)};
+        const u32x2 pk = {pack2<T>(fmaf(dsk, sv, yv.x), yv.y), pack2<T>(yv.z, yv.w)};
         *(u32x2*)(a.y + ((xrow0 + tid) * a.Dm + d) * 4) = pk;
       }
     }
@@ -501,23 +514,24 @@ __global__ __launch_bounds__(kThreads) void fused_bc_ssm_kernel(FusedArgs a) {
   }
 }
 
-// The split walk's second launch: y = bf16(p0 + p1 + (D s, 0, 0, 0)) per (b, t, d), the
+// The split walk's second launch: y = T(p0 + p1 + (D s, 0, 0, 0)) per (b, t, d), the
 // sum in the order the unsplit kernel makes it (half 0's partial, then half 1's, then
 // D s), so both forms give the same y bit for bit.
+template <typename T>
 __global__ __launch_bounds__(256) void fused_bc_combine_kernel(const float* __restrict__ ypart,
-                                                               const bf16_t* __restrict__ s,
+                                                               const uint16_t* __restrict__ s,
                                                                const float* __restrict__ dvec,
-                                                               __bf16* __restrict__ y,
+                                                               uint16_t* __restrict__ y,
                                                                int64_t n, int64_t half_stride,
                                                                int Dm) {
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
        e += (int64_t)gridDim.x * blockDim.x) {
     const float4 p0 = *(const float4*)(ypart + e * 4);
     const float4 p1 = *(const float4*)(ypart + (half_stride + e) * 4);
-    const float sv = io<bf16_t>::to_f32(s[e]);
+    const float sv = io<T>::bits_to_f32(s[e]);
     const float dsk = dvec[e % Dm];
-    const u32x2 pk = {pk_bf16(fmaf(dsk, sv, p0.x + p1.x), p0.y + p1.y),
-                      pk_bf16(p0.z + p1.z, p0.w + p1.w)};
+    const u32x2 pk = {pack2<T>(fmaf(dsk, sv, p0.x + p1.x), p0.y + p1.y),
+                      pack2<T>(p0.z + p1.z, p0.w + p1.w)};
     *(u32x2*)(y + e * 4) = pk;
   }
 }
@@ -536,6 +550,27 @@ int set_lds_limit(K kernel) {
   return (int)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   kLdsFused);
 }
+
+template <typename T>
+int set_lds_limits() {
+  int st = set_lds_limit(fused_bc_ssm_kernel<T, true, true>);
+  if (st == MQC_OK) st = set_lds_limit(fused_bc_ssm_kernel<T, true, false>);
+  if (st == MQC_OK) st = set_lds_limit(fused_bc_ssm_kernel<T, false, true>);
+  if (st == MQC_OK) st = set_lds_limit(fused_bc_ssm_kernel<T, false, false>);
+  return st;
+}
+
+template <typename T>
+void launch_fused(const FusedArgs& a, dim3 grid, bool full_t, bool full_s, hipStream_t st) {
+  if (full_t && full_s)
+    hipLaunchKernelGGL((fused_bc_ssm_kernel<T, true, true>), grid, dim3(kThreads), kLdsFused, st, a);
+  else if (full_t)
+    hipLaunchKernelGGL((fused_bc_ssm_kernel<T, true, false>), grid, dim3(kThreads), kLdsFused, st, a);
+  else if (full_s)
+    hipLaunchKernelGGL((fused_bc_ssm_kernel<T, false, true>), grid, dim3(kThreads), kLdsFused, st, a);
+  else
+    hipLaunchKernelGGL((fused_bc_ssm_kernel<T, false, false>), grid, dim3(kThreads), kLdsFused, st, a);
+}
 }  // namespace
 
 namespace {
@@ -552,7 +587,7 @@ int fused_bc_run(const void* x, const void* B_weight, const void* C_weight, cons
                  bool split, void* workspace, int64_t workspace_bytes, void* stream) {
   if (batch < 0 || seq_len < 0 || d_inner < 0 || d_state < 0) return MQC_E_SHAPE;
   if (dtype != MQC_F32 && dtype != MQC_BF16 && dtype != MQC_F16) return MQC_E_DTYPE;
-  if (dtype != MQC_BF16) return MQC_E_DTYPE;  // bf16 MFMAs only
+  if (dtype == MQC_F32) return MQC_E_DTYPE;  // 16-bit MFMAs only
   if (batch == 0 || d_inner == 0) return MQC_OK;
   if (d_state < 1 || d_state > kMaxHalves * kHalf) return MQC_E_LIMIT;
   if (d_state % 2 != 0) return MQC_E_SHAPE;  // 8-row DMA groups of whole states
@@ -586,18 +621,16 @@ int fused_bc_run(const void* x, const void* B_weight, const void* C_weight, cons
   if (e != hipSuccess) return (int)e;
   if (dev < 0 || dev >= kMaxDevices) return MQC_E_LIMIT;
   if (!g_fused_attr_set[dev].load(std::memory_order_acquire)) {
-    int st = set_lds_limit(fused_bc_ssm_kernel<true, true>);
-    if (st == MQC_OK) st = set_lds_limit(fused_bc_ssm_kernel<true, false>);
-    if (st == MQC_OK) st = set_lds_limit(fused_bc_ssm_kernel<false, true>);
-    if (st == MQC_OK) st = set_lds_limit(fused_bc_ssm_kernel<false, false>);
+    int st = set_lds_limits<bf16_t>();
+    if (st == MQC_OK) st = set_lds_limits<f16_t>();
     if (st != MQC_OK) return st;
     g_fused_attr_set[dev].store(true, std::memory_order_release);
   }
   FusedArgs a{};
-  a.x = (const __bf16*)x; a.wb = (const __bf16*)B_weight; a.wc = (const __bf16*)C_weight;
-  a.delta = (const bf16_t*)delta; a.s = (const bf16_t*)s;
+  a.x = (const uint16_t*)x; a.wb = (const uint16_t*)B_weight; a.wc = (const uint16_t*)C_weight;
+  a.delta = (const uint16_t*)delta; a.s = (const uint16_t*)s;
   a.lam_alpha = lambda_alpha; a.lam_imag = lambda_imag; a.dvec = D;
-  a.h0 = (const float*)h0; a.y = (__bf16*)y; a.h_last = (float*)h_last;
+  a.h0 = (const float*)h0; a.y = (uint16_t*)y; a.h_last = (float*)h_last;
   a.ypart = split ? (float*)workspace : nullptr;
   a.batch = (int)batch; a.T = (int)seq_len; a.Dm = (int)d_inner; a.S = (int)d_state; a.eps = eps;
   a.split = split ? 1 : 0;
@@ -605,22 +638,23 @@ int fused_bc_run(const void* x, const void* B_weight, const void* C_weight, cons
   const dim3 grid((unsigned)units);
   hipStream_t st = (hipStream_t)stream;
   const bool full_t = seq_len % kT == 0, full_s = d_state % kHalf == 0;
-  if (full_t && full_s)
-    hipLaunchKernelGGL((fused_bc_ssm_kernel<true, true>), grid, dim3(kThreads), kLdsFused, st, a);
-  else if (full_t)
-    hipLaunchKernelGGL((fused_bc_ssm_kernel<true, false>), grid, dim3(kThreads), kLdsFused, st, a);
-  else if (full_s)
-    hipLaunchKernelGGL((fused_bc_ssm_kernel<false, true>), grid, dim3(kThreads), kLdsFused, st, a);
+  if (dtype == MQC_BF16)
+    launch_fused<bf16_t>(a, grid, full_t, full_s, st);
   else
-    hipLaunchKernelGGL((fused_bc_ssm_kernel<false, false>), grid, dim3(kThreads), kLdsFused, st, a);
+    launch_fused<f16_t>(a, grid, full_t, full_s, st);
   if (!split) return launch_status();
   int status = launch_status();
   if (status != MQC_OK) return status;
   const int64_t n = batch * seq_len * d_inner;
   const int64_t blocks = (n + 255) / 256 < 16384 ? (n + 255) / 256 : 16384;
-  hipLaunchKernelGGL(fused_bc_combine_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                     (const float*)workspace, (const bf16_t*)s, D, (__bf16*)y, n, n,
-                     (int)d_inner);
+  if (dtype == MQC_BF16)
+    hipLaunchKernelGGL(fused_bc_combine_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const float*)workspace, (const uint16_t*)s, D, (uint16_t*)y, n, n,
+                       (int)d_inner);
+  else
+    hipLaunchKernelGGL(fused_bc_combine_kernel<f16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const float*)workspace, (const uint16_t*)s, D, (uint16_t*)y, n, n,
+                       (int)d_inner);
   return launch_status();
 }
 

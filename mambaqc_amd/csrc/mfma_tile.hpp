@@ -1,11 +1,12 @@
 #pragma once
-// The MFMA main loop shared by the library's bf16 GEMM tiles (gfx950):
+// The MFMA main loop shared by the library's 16-bit GEMM tiles (gfx950; bf16 or fp16
+// operands, E = __bf16 or _Float16):
 //   acc += W_tile[TW rows, K] . X_tile[TX rows, K]^T
 // for one output tile, fp32 accumulation. Described here for the 256 x 256 tile of the
 // projections (Tile256); TileCfg gives smaller tiles the same loop.
 //
 //   - 8 waves (two per SIMD); wave w owns W rows (w >> 2) * 128 + [0, 128) and X rows
-//     (w & 3) * 64 + [0, 64) as 8 x 4 blocks of v_mfma_f32_16x16x32_bf16 accumulators
+//     (w & 3) * 64 + [0, 64) as 8 x 4 blocks of v_mfma_f32_16x16x32_bf16 (_f16) accumulators
 //     (128 fp32 per lane). W rows are the MFMA's first operand and X rows its second, so
 //     in block (nb, mb) lane l holds the 4 consecutive W rows
 //     (w >> 2) * 128 + nb * 16 + 4 * (l >> 4) + [0, 4) of X row (w & 3) * 64 + mb * 16 +
@@ -30,6 +31,7 @@ namespace mqc {
 namespace mfma {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -67,6 +69,17 @@ __device__ inline uint32_t pk_bf16(float a, float b) {
   typedef __bf16 h16x2 __attribute__((ext_vector_type(2)));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, h16x2));
 }
+
+// One 16 x 16 x 32 MFMA of 16-bit operands into fp32, by operand type.
+__device__ inline floatx4 mfma16(const bf16x8& a, const bf16x8& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ inline floatx4 mfma16(const f16x8& a, const f16x8& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+template <typename E> struct FragOf;
+template <> struct FragOf<__bf16> { using type = bf16x8; };
+template <> struct FragOf<_Float16> { using type = f16x8; };
 
 // s_waitcnt vmcnt(N) with expcnt and lgkmcnt at their maxima (gfx9 fields).
 template <int N>
@@ -156,7 +169,7 @@ __device__ inline void tile_issue_stage(int kt, int wave, uint32_t lds0, const D
   }
 }
 
-template <typename Cfg, typename WRow, typename XRow>
+template <typename Cfg, typename E = __bf16, typename WRow, typename XRow>
 __device__ inline void tile_kloop_cfg(int K, char* lds,
                                       floatx4 (&acc)[Cfg::WB][Cfg::XB], const WRow& wrow,
                                       const XRow& xrow) {
@@ -183,19 +196,20 @@ __device__ inline void tile_kloop_cfg(int K, char* lds,
     const int rx = wm * (Cfg::TX / Cfg::NW_X) + rl;
     xoff[kk] = Cfg::kWBytes + rx * kRowBytes + gswz(rx, c) * 16;
   }
-  bf16x8 wf[2][WB], xf[2][XB];
+  using frag = typename FragOf<E>::type;
+  frag wf[2][WB], xf[2][XB];
   auto read_frags = [&](int buf, const char* sb, int kk) {
 #pragma unroll
-    for (int nb = 0; nb < WB; ++nb) wf[buf][nb] = *(const bf16x8*)(sb + woff[kk] + nb * 16 * kRowBytes);
+    for (int nb = 0; nb < WB; ++nb) wf[buf][nb] = *(const frag*)(sb + woff[kk] + nb * 16 * kRowBytes);
 #pragma unroll
-    for (int mb = 0; mb < XB; ++mb) xf[buf][mb] = *(const bf16x8*)(sb + xoff[kk] + mb * 16 * kRowBytes);
+    for (int mb = 0; mb < XB; ++mb) xf[buf][mb] = *(const frag*)(sb + xoff[kk] + mb * 16 * kRowBytes);
   };
   auto mfmas = [&](int buf) {
 #pragma unroll
     for (int nb = 0; nb < WB; ++nb)
 #pragma unroll
       for (int mb = 0; mb < XB; ++mb)
-        acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[buf][nb], xf[buf][mb], acc[nb][mb], 0, 0, 0);
+        acc[nb][mb] = mfma16(wf[buf][nb], xf[buf][mb], acc[nb][mb]);
   };
 
   const int KT = K / kBK;
@@ -222,11 +236,11 @@ __device__ inline void tile_kloop_cfg(int K, char* lds,
   }
 }
 
-// The 256 x 256 tile's K loop.
-template <typename WRow, typename XRow>
+// The 256 x 256 tile's K loop (E: the operands' 16-bit type).
+template <typename E = __bf16, typename WRow, typename XRow>
 __device__ inline void tile_kloop(int K, char* lds, floatx4 (&acc)[kWB][kXB], const WRow& wrow,
                                   const XRow& xrow) {
-  tile_kloop_cfg<Tile256>(K, lds, acc, wrow, xrow);
+  tile_kloop_cfg<Tile256, E>(K, lds, acc, wrow, xrow);
 }
 
 }  // namespace mfma

@@ -497,13 +497,14 @@ FUSED_BC_SPLIT_WS_MAX = 4 << 30
 
 def fused_bc_eligible(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torch.Tensor,
                       d_state: int) -> bool:
-    """Whether ssm_forward_fused_bc takes these operands: bf16 x [batch, T, d_inner]
-    with d_inner a multiple of 64, bf16 weights [d_inner * d_state * 4, d_inner] of
-    one shape, d_state even and at most 64, all on a ROCm device."""
+    """Whether ssm_forward_fused_bc takes these operands: x [batch, T, d_inner] with
+    d_inner a multiple of 64 and weights [d_inner * d_state * 4, d_inner] of one shape,
+    all bf16 or all fp16, d_state even and at most 64, all on a ROCm device."""
     if x.dim() != 3 or not (x.is_cuda and B_weight.is_cuda and C_weight.is_cuda):
         return False
     d_inner = x.shape[-1]
-    return (x.dtype == B_weight.dtype == C_weight.dtype == torch.bfloat16
+    return (x.dtype == B_weight.dtype == C_weight.dtype
+            and x.dtype in (torch.bfloat16, torch.float16)
             and d_inner % 64 == 0 and 0 < d_state <= 64 and d_state % 2 == 0
             and tuple(B_weight.shape) == tuple(C_weight.shape) == (d_inner * d_state * 4, d_inner))
 
@@ -513,17 +514,19 @@ def ssm_forward_fused_bc(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torc
                          lambda_imag: torch.Tensor, D: torch.Tensor, eps: float = 1e-6,
                          h0: torch.Tensor | None = None, return_state: bool = False,
                          split: bool | None = None):
-    """The block's B/C projections and its SSM in one HIP launch (inference, bf16).
+    """The block's B/C projections and its SSM in one HIP launch (inference, bf16 or
+    fp16).
 
     B = x B_weight^T and C = x C_weight^T, as [batch, seq_len, d_inner, d_state, 4]
     (the bias-free real -> quaternion projections,
     mambaqc/layers/quaternion_linear.py:145-161), are computed 256 tokens at a time
-    on chip, rounded to bf16 as the projections would store them, and walked there
-    by ssm_forward_fused_dl's recurrence; neither is ever written to memory.
-    x: [batch, seq_len, d_inner] bf16 (the projections' input); B_weight, C_weight:
-    [d_inner * d_state * 4, d_inner] bf16; delta, s, the Lambda parameters, D and h0
-    as in ssm_forward_fused_dl. Returns y [batch, seq_len, d_inner, 4] bf16 (and the
-    final fp32 state if return_state). Inference only (no autograd).
+    on chip, rounded to x's dtype as the projections would store them, and walked
+    there by ssm_forward_fused_dl's recurrence; neither is ever written to memory.
+    x: [batch, seq_len, d_inner] bf16 or fp16 (the projections' input); B_weight,
+    C_weight: [d_inner * d_state * 4, d_inner] in x's dtype; delta, s (taken in x's
+    dtype), the Lambda parameters, D and h0 as in ssm_forward_fused_dl. Returns y
+    [batch, seq_len, d_inner, 4] in x's dtype (and the final fp32 state if
+    return_state). Inference only (no autograd).
     split: run each half of the states (32) in a workgroup of its own, with a
     workspace for the halves' partial sums and a second launch adding them (the
     same y bit for bit); None splits batches of at most FUSED_BC_SPLIT_MAX_BATCH.
@@ -546,15 +549,16 @@ def ssm_forward_fused_bc(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torc
             x, B_weight, C_weight, delta, s, lambda_alpha, lambda_imag, D)):
         raise RuntimeError("ssm_forward_fused_bc: inference only; run under torch.no_grad")
     if not fused_bc_eligible(x, B_weight, C_weight, d_state):
-        raise ValueError("ssm_forward_fused_bc: needs bf16 x [batch, T, d_inner] with d_inner a "
-                         "multiple of 64, bf16 weights [d_inner * d_state * 4, d_inner] and an "
-                         "even d_state <= 64")
-    bf = torch.bfloat16
+        raise ValueError("ssm_forward_fused_bc: needs bf16 or fp16 x [batch, T, d_inner] with "
+                         "d_inner a multiple of 64, weights [d_inner * d_state * 4, d_inner] of "
+                         "x's dtype and an even d_state <= 64")
+    dt = x.dtype
     xc, wb, wc = (nat.aligned16(t.detach()) for t in (x, B_weight, C_weight))
-    dl, sv = (nat.aligned16(t.detach().to(bf)) for t in (delta, s))
+    dl, sv = (nat.aligned16(t.detach().to(dt)) for t in (delta, s))
     la, li, Dv = (nat.param_f32(t) for t in (lambda_alpha, lambda_imag, D))
     h0c = None if h0 is None else nat.aligned16(h0.detach().float())
-    y = torch.empty(batch, T, d_inner, 4, device=x.device, dtype=bf)
+    y = torch.empty(batch, T, d_inner, 4, device=x.device, dtype=dt)
+    code = nat.dtype_code(xc)
     h_last = (torch.empty(batch, d_inner, d_state, 4, device=x.device, dtype=torch.float32)
               if return_state else None)
     if split is None:
@@ -566,7 +570,7 @@ def ssm_forward_fused_bc(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torc
         nat.call("mqc_ssm_fused_bc_fwd", xc, xc.data_ptr(), wb.data_ptr(), wc.data_ptr(),
                  dl.data_ptr(), sv.data_ptr(), la.data_ptr(), li.data_ptr(), Dv.data_ptr(),
                  nat.ptr(h0c), y.data_ptr(), nat.ptr(h_last), batch, T, d_inner, d_state,
-                 float(eps), nat.BF16, stream)
+                 float(eps), code, stream)
         return (y, h_last) if return_state else y
     # Split: one launch over the whole sequence, or (a batch of one whose workspace
     # would pass FUSED_BC_SPLIT_WS_MAX) segments of whole 256-token tiles.
@@ -590,7 +594,7 @@ def ssm_forward_fused_bc(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torc
                  wc.data_ptr(), dl[:, t0:t1].data_ptr(), sv[:, t0:t1].data_ptr(),
                  la.data_ptr(), li.data_ptr(), Dv.data_ptr(),
                  nat.ptr(h0c) if t0 == 0 else state.data_ptr(), y[:, t0:t1].data_ptr(),
-                 nat.ptr(state), batch, t1 - t0, d_inner, d_state, float(eps), nat.BF16,
+                 nat.ptr(state), batch, t1 - t0, d_inner, d_state, float(eps), code,
                  ws.data_ptr(), ws_bytes, stream)
     return (y, h_last) if return_state else y
 

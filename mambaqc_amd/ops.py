@@ -170,8 +170,8 @@ def ssm_forward_fused_bc(x: Tensor, B_weight: Tensor, C_weight: Tensor, delta: T
                          lambda_alpha: Tensor, lambda_imag: Tensor, D: Tensor,
                          h0: Optional[Tensor] = None,
                          eps: float = 1e-6) -> Tuple[Tensor, Tensor]:
-    """The B/C projections and the inference walk in one kernel (bf16):
-    (y [B, T, D, 4] bf16, h_last [B, D, S, 4] fp32). Inference only."""
+    """The B/C projections and the inference walk in one kernel (bf16 or fp16):
+    (y [B, T, D, 4] in x's dtype, h_last [B, D, S, 4] fp32). Inference only."""
     with torch.no_grad():
         return sf.ssm_forward_fused_bc(x, B_weight, C_weight, delta, s, lambda_alpha, lambda_imag,
                                        D, eps=eps, h0=h0, return_state=True)

@@ -2,9 +2,9 @@
 kernels.ssm_forward_fused_bc) against the CPU oracle and against the unfused
 path (torch's GEMMs for B and C, then mqc_ssm_fused_fwd).
 
-The oracle side: B = x W_B^T and C = x W_C^T in fp32 from the same bf16
-operands, rounded to bf16 (the dtype the projections store and the fused kernel
-rounds to on chip), then oracle.ssm_forward_dl_reference in float64. bf16
+The oracle side: B = x W_B^T and C = x W_C^T in fp32 from the same 16-bit
+operands, rounded to their dtype (what the projections store and the fused kernel
+rounds to on chip), then oracle.ssm_forward_dl_reference in float64. bf16 and fp16
 tolerance 2e-2 with the atol floor of rtol * max|ref| (conftest.assert_close).
 """
 import ctypes
@@ -22,17 +22,18 @@ from mambaqc_amd.kernels.ssm_fused import fused_bc_eligible
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 BF = torch.bfloat16
+F16 = torch.float16
 
 
-def _inputs(b, T, d, k, seed, w_std=None):
+def _inputs(b, T, d, k, seed, w_std=None, dt=BF):
     g = torch.Generator(device=DEV).manual_seed(seed)
     r = lambda *s: torch.randn(*s, generator=g, device=DEV)
     w_std = 0.3 / d ** 0.5 if w_std is None else w_std
-    x = r(b, T, d).to(BF)
-    wb = (r(d * k * 4, d) * w_std).to(BF)
-    wc = (r(d * k * 4, d) * w_std).to(BF)
-    delta = torch.nn.functional.softplus(r(b, T, d) - 1).to(BF)
-    s = r(b, T, d).to(BF)
+    x = r(b, T, d).to(dt)
+    wb = (r(d * k * 4, d) * w_std).to(dt)
+    wc = (r(d * k * 4, d) * w_std).to(dt)
+    delta = torch.nn.functional.softplus(r(b, T, d) - 1).to(dt)
+    s = r(b, T, d).to(dt)
     la = r(d, k) * 0.5 + 1
     li = r(d, k, 3) * 0.3
     D = 1 + 0.1 * r(d)
@@ -42,10 +43,11 @@ def _inputs(b, T, d, k, seed, w_std=None):
 
 def _bc_rounded(x, w, d_slice, k):
     """B (or C) for the d's of d_slice, as the projections store it: fp32 GEMM of
-    the bf16 operands, rounded to bf16; [b, T, n_d, k, 4] in float64 on the CPU."""
+    the 16-bit operands, rounded to their dtype; [b, T, n_d, k, 4] in float64 on
+    the CPU."""
     b, T, d = x.shape
     rows = w.view(d, k * 4, d)[d_slice].reshape(-1, d)
-    out = (x.float().reshape(-1, d) @ rows.float().t()).to(BF)
+    out = (x.float().reshape(-1, d) @ rows.float().t()).to(x.dtype)
     return out.double().cpu().view(b, T, -1, k, 4)
 
 
@@ -70,26 +72,28 @@ def _oracle(x, wb, wc, delta, s, la, li, D, h0, d_slice, b_slice=slice(None), ep
     (1, 1, 128, 2),      # one token, two states
 ])
 @pytest.mark.parametrize("with_h0", [False, True])
-def test_fused_bc_vs_oracle(shape, with_h0):
+@pytest.mark.parametrize("dt", [BF, F16], ids=["bf16", "f16"])
+def test_fused_bc_vs_oracle(shape, with_h0, dt):
     b, T, d, k = shape
-    print(f"fused_bc vs oracle {shape} h0={with_h0}", flush=True)
-    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=sum(shape))
+    print(f"fused_bc vs oracle {shape} h0={with_h0} {dt}", flush=True)
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=sum(shape), dt=dt)
     h0 = h0 if with_h0 else None
     assert fused_bc_eligible(x, wb, wc, k)
     with torch.no_grad():
         y, h = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0, return_state=True)
     want_y, want_h = _oracle(x, wb, wc, delta, s, la, li, D, h0, slice(None))
-    assert y.dtype == BF and h.dtype == torch.float32
+    assert y.dtype == dt and h.dtype == torch.float32
     assert_close(y, want_y, 2e-2, f"fused y {shape}")
     assert_close(h, want_h, 2e-2, f"fused h_last {shape}")
 
 
-def test_fused_bc_equals_unfused_path_small():
-    """Against the unfused path on the same weights (torch's bf16 GEMMs, then the
+@pytest.mark.parametrize("dt", [BF, F16], ids=["bf16", "f16"])
+def test_fused_bc_equals_unfused_path_small(dt):
+    """Against the unfused path on the same weights (torch's 16-bit GEMMs, then the
     library's walk): the same recurrence on B and C that differ at most by the
     rounding of differently ordered fp32 sums."""
     b, T, d, k = 2, 700, 128, 64
-    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=5)
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=5, dt=dt)
     with torch.no_grad():
         y, h = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0, return_state=True)
         Bq = torch.nn.functional.linear(x, wb).view(b, T, d, k, 4)
@@ -156,6 +160,8 @@ def test_fused_bc_state_in_place_and_empty():
 def test_fused_bc_rejects_what_it_cannot_run():
     x, wb, wc, delta, s, la, li, D, _ = _inputs(1, 16, 64, 4, seed=3)
     assert not fused_bc_eligible(x.float(), wb.float(), wc.float(), 4)
+    assert not fused_bc_eligible(x.half(), wb, wc, 4)  # mixed 16-bit dtypes
+    assert fused_bc_eligible(x.half(), wb.half(), wc.half(), 4)
     assert not fused_bc_eligible(x, wb, wc, 3)
     with pytest.raises(ValueError):
         K.ssm_forward_fused_bc(x.float(), wb.float(), wc.float(), delta, s, la, li, D)
@@ -205,13 +211,14 @@ def test_block_forward_fused_bc_path():
     ((1, 256, 64, 32), False),    # one half: the split call is the one-launch form
     ((1, 1, 64, 64), True),       # one token
 ])
-def test_fused_bc_split_equals_one_launch(shape, with_h0):
+@pytest.mark.parametrize("dt", [BF, F16], ids=["bf16", "f16"])
+def test_fused_bc_split_equals_one_launch(shape, with_h0, dt):
     """Each half of the states in a workgroup of its own, partial sums added by a
     second launch (mqc_ssm_fused_bc_fwd_split): y and h_last equal the one-launch
-    form bit for bit, and the oracle to bf16 tolerance."""
+    form bit for bit, and the oracle to 16-bit tolerance."""
     b, T, d, k = shape
-    print(f"fused_bc split {shape} h0={with_h0}", flush=True)
-    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=11 + sum(shape))
+    print(f"fused_bc split {shape} h0={with_h0} {dt}", flush=True)
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=11 + sum(shape), dt=dt)
     h0 = h0 if with_h0 else None
     with torch.no_grad():
         y1, h1 = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0,
@@ -302,15 +309,41 @@ def test_fused_bc_split_in_time_segments(monkeypatch):
 
 
 @pytest.mark.parametrize("split", [False, True])
-def test_fused_bc_eps_clamp(split):
+@pytest.mark.parametrize("dt", [BF, F16], ids=["bf16", "f16"])
+def test_fused_bc_eps_clamp(split, dt):
     """An eps large enough that the clamp max(N, eps) of the Cayley map engages on
     the steps with small delta (N = 1 - delta a + delta^2 |Lambda|^2 / 4 >= 1 here,
     eps 1.6): the fused walk, in both forms, against the oracle with the same eps."""
     b, T, d, k = 1, 300, 64, 64
-    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=41)
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=41, dt=dt)
     with torch.no_grad():
         y, h = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, eps=1.6, h0=h0,
                                       return_state=True, split=split)
     want_y, want_h = _oracle(x, wb, wc, delta, s, la, li, D, h0, slice(None), eps=1.6)
     assert_close(y, want_y, 2e-2, "fused y, eps clamp")
     assert_close(h, want_h, 2e-2, "fused h_last, eps clamp")
+
+
+@pytest.mark.parametrize("rows", [2, 1])
+def test_block_forward_fused_bc_fp16(rows):
+    """An fp16 block (converted with .half(), no autocast) takes the fused path too,
+    one workgroup per d at a batch of two and split halves at a batch of one: against
+    the same block unfused and the CPU oracle of the block."""
+    import mambaqc_amd
+
+    torch.manual_seed(6)
+    blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=64).to(DEV, F16).eval()
+    g = torch.Generator(device=DEV).manual_seed(7)
+    x = torch.randn(rows, 300, 64, generator=g, device=DEV).to(F16)
+    assert blk._use_fused_bc(torch.empty(rows, 300, blk.d_inner, device=DEV, dtype=F16))
+    print(f"fp16 block fused B{rows}", flush=True)
+    with torch.no_grad():
+        got = blk(x)
+        blk.fuse_bc = False
+        ref_unfused = blk(x)
+        blk.fuse_bc = None
+    assert got.dtype == F16
+    assert_close(got, ref_unfused, 2e-2, "fp16 block fused vs unfused")
+    sd = {k: v.detach().float().cpu() for k, v in blk.state_dict().items()}
+    want = oracle.block_forward_reference(sd, x.float().cpu(), d_state=64)
+    assert_close(got, want, 2e-2, "fp16 block fused vs oracle")

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     lib = nat.load()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mqc_abi_version() == nat.ABI_VERSION == 7
+    assert lib.mqc_abi_version() == nat.ABI_VERSION == 8
 
 
 def test_status_strings():
@@ -293,15 +293,18 @@ def test_fused_bc_split_workspace_without_gpu():
 
 
 def test_fused_bc_validation_without_gpu():
-    """mqc_ssm_fused_bc_fwd refuses, before any HIP call: a dtype other than bf16,
-    d_state odd or above 64, d_inner not a multiple of 64, NULL operands and
-    misaligned pointers; nothing to do is not an error."""
+    """mqc_ssm_fused_bc_fwd refuses, before any HIP call: fp32 or an unknown dtype
+    (it runs bf16 and fp16), d_state odd or above 64, d_inner not a multiple of 64,
+    NULL operands and misaligned pointers; nothing to do is not an error."""
     lib = nat.load()
     bf = 1
     odd = ctypes.c_void_p(4096 + 8)
     P = [FAKE] * 8  # x, W_B, W_C, delta, s, lambda_alpha, lambda_imag, D
     # (…, h0, y, h_last, batch, seq_len, d_inner, d_state, eps, dtype, stream)
     assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, 1, 16, 64, 64, 1e-6, 0, None) == -3
+    assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, 1, 16, 64, 64, 1e-6, 3, None) == -3
+    # fp16 passes the dtype check and stops at the next one (d_state odd).
+    assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, 1, 16, 64, 63, 1e-6, 2, None) == -2
     assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, 1, 16, 64, 63, 1e-6, bf, None) == -2
     assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, 1, 16, 64, 66, 1e-6, bf, None) == -5
     assert lib.mqc_ssm_fused_bc_fwd(*P, None, FAKE, None, 1, 16, 96, 64, 1e-6, bf, None) == -2
