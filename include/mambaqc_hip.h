@@ -264,8 +264,8 @@ int mqc_out_proj_gate_fwd(const void* y, const void* W, const void* bias, const 
                           const void* z, int64_t z_row_stride, void* out, int64_t rows,
                           int64_t d_model, int64_t k, int dtype, void* stream);
 
-/* C[M, N] = X[M, K] . W[N, K]^T in bf16 with fp32 accumulation (dtype must be
- * MQC_BF16), contiguous row-major X, W, C, 16-byte aligned; N a multiple of
+/* C[M, N] = X[M, K] . W[N, K]^T in bf16 or fp16 (dtype MQC_BF16 or MQC_F16) with
+ * fp32 accumulation, contiguous row-major X, W, C, 16-byte aligned; N a multiple of
  * 256, K of 64, M any. The hand-written MFMA GEMM of the block's B/C
  * projections (F.linear, mambaqc/layers/quaternion_linear.py:145-161, called
  * at mambaqc/models/quaternion_mamba2_block.py:186-191), the first stage of

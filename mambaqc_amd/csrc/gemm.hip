@@ -1,5 +1,5 @@
-// Hand-written MFMA GEMM for the block's B/C projections (bf16):
-//   C[M, N] = X[M, K] . W[N, K]^T,  fp32 accumulation, bf16 output,
+// Hand-written MFMA GEMM for the block's B/C projections (bf16 or fp16):
+//   C[M, N] = X[M, K] . W[N, K]^T,  fp32 accumulation, output in the operands' type,
 // the nn.Linear layout of mambaqc/layers/quaternion_linear.py:145-161
 // (F.linear(x, W) for the real -> quaternion maps B_proj and C_proj,
 // models/quaternion_mamba2_block.py:186-191).
@@ -10,7 +10,7 @@
 // which is faster at the config-3 shape (M 8192, N 393216, K 1536).
 //
 // Tiling (gfx950): the 256 x 256 MFMA main loop of mfma_tile.hpp (8 waves, two 64 KB
-// LDS stages filled by global->LDS DMA, 16 x 16 x 32 bf16 MFMAs), plus:
+// LDS stages filled by global->LDS DMA, 16 x 16 x 32 bf16 or fp16 MFMAs), plus:
 //   - Tiles in launch order with the M tile fastest: the 256 tiles in flight cover all of X
 //     (in the Infinity Cache) and a few W tiles, each of which is read from HBM about once.
 //   - Epilogue through LDS: the tile is written to LDS in the MFMA layout (rows of 512 bytes,
@@ -32,12 +32,14 @@ constexpr int kGBK = kBK;
 constexpr int kGThreads = kThreads;
 constexpr int kLdsBytes = kStagesBytes;  // two stages = 128 KB (also the epilogue tile)
 
-// One 256 x 256 tile. FULL_M: all 256 rows of the tile exist (every row tile but a
-// ragged last one, whose rows past M read row M - 1).
-template <bool FULL_M>
-__device__ inline void gemm_tile(const __bf16* __restrict__ X, const __bf16* __restrict__ W,
-                                 __bf16* __restrict__ C, int M, int N, int K, int m0, int n0,
+// One 256 x 256 tile. T: the 16-bit storage type (bf16_t or f16_t). FULL_M: all 256
+// rows of the tile exist (every row tile but a ragged last one, whose rows past M read
+// row M - 1).
+template <typename T, bool FULL_M>
+__device__ inline void gemm_tile(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
+                                 uint16_t* __restrict__ C, int M, int N, int K, int m0, int n0,
                                  char* lds) {
+  using E = typename std::conditional<std::is_same<T, bf16_t>::value, __bf16, _Float16>::type;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -66,7 +68,7 @@ __device__ inline void gemm_tile(const __bf16* __restrict__ X, const __bf16* __r
       return X + ((int64_t)gb * K + k0);
     }
   };
-  tile_kloop(K, lds, acc, wrow, xrow);
+  tile_kloop<E>(K, lds, acc, wrow, xrow);
 
   // Epilogue through LDS (every wave is past its last LDS read at the barrier).
   wait_lgkm0();
@@ -78,7 +80,7 @@ __device__ inline void gemm_tile(const __bf16* __restrict__ X, const __bf16* __r
       const int ml = wm * 64 + mb * 16 + rl;
       const int nl = wn * 128 + nb * 16 + 4 * q;
       const floatx4& v = acc[nb][mb];
-      const u32x2 pk = {pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])};
+      const u32x2 pk = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
       *(u32x2*)(lds + ml * 512 + ((nl >> 3) ^ (ml & 31)) * 16 + (nl & 7) * 2) = pk;
     }
   wait_lgkm0();
@@ -94,18 +96,19 @@ __device__ inline void gemm_tile(const __bf16* __restrict__ X, const __bf16* __r
   }
 }
 
-__global__ __launch_bounds__(kGThreads) void gemm_nt_bf16_kernel(const __bf16* __restrict__ X,
-                                                                  const __bf16* __restrict__ W,
-                                                                  __bf16* __restrict__ C, int M,
-                                                                  int N, int K) {
+template <typename T>
+__global__ __launch_bounds__(kGThreads) void gemm_nt_kernel(const uint16_t* __restrict__ X,
+                                                             const uint16_t* __restrict__ W,
+                                                             uint16_t* __restrict__ C, int M,
+                                                             int N, int K) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int mt = (M + kGT - 1) / kGT;
   const int m0 = (int)(blockIdx.x % mt) * kGT;
   const int n0 = (int)(blockIdx.x / mt) * kGT;
   if (m0 + kGT <= M)
-    gemm_tile<true>(X, W, C, M, N, K, m0, n0, lds);
+    gemm_tile<T, true>(X, W, C, M, N, K, m0, n0, lds);
   else
-    gemm_tile<false>(X, W, C, M, N, K, m0, n0, lds);
+    gemm_tile<T, false>(X, W, C, M, N, K, m0, n0, lds);
 }
 
 }  // namespace
@@ -124,7 +127,7 @@ int mqc_gemm_nt(const void* X, const void* W, void* C, int64_t M, int64_t N, int
                 void* stream) {
   if (M < 0 || N < 0 || K < 0) return MQC_E_SHAPE;
   if (dtype != MQC_F32 && dtype != MQC_BF16 && dtype != MQC_F16) return MQC_E_DTYPE;
-  if (dtype != MQC_BF16) return MQC_E_DTYPE;  // bf16 only
+  if (dtype == MQC_F32) return MQC_E_DTYPE;  // 16-bit MFMAs only
   if (M == 0 || N == 0) return MQC_OK;
   if (K == 0 || N % kGT != 0 || K % kGBK != 0) return MQC_E_SHAPE;
   if (!X || !W || !C) return MQC_E_NULL;
@@ -140,14 +143,22 @@ int mqc_gemm_nt(const void* X, const void* W, void* C, int64_t M, int64_t N, int
   if (e != hipSuccess) return (int)e;
   if (dev < 0 || dev >= kMaxDevices) return MQC_E_LIMIT;
   if (!g_lds_attr_set[dev].load(std::memory_order_acquire)) {
-    e = hipFuncSetAttribute((const void*)gemm_nt_bf16_kernel,
+    e = hipFuncSetAttribute((const void*)gemm_nt_kernel<bf16_t>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)gemm_nt_kernel<f16_t>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return (int)e;
     g_lds_attr_set[dev].store(true, std::memory_order_release);
   }
-  hipLaunchKernelGGL(gemm_nt_bf16_kernel, dim3((unsigned)tiles), dim3(kGThreads), kLdsBytes,
-                     (hipStream_t)stream, (const __bf16*)X, (const __bf16*)W, (__bf16*)C, (int)M,
-                     (int)N, (int)K);
+  if (dtype == MQC_BF16)
+    hipLaunchKernelGGL(gemm_nt_kernel<bf16_t>, dim3((unsigned)tiles), dim3(kGThreads), kLdsBytes,
+                       (hipStream_t)stream, (const uint16_t*)X, (const uint16_t*)W, (uint16_t*)C,
+                       (int)M, (int)N, (int)K);
+  else
+    hipLaunchKernelGGL(gemm_nt_kernel<f16_t>, dim3((unsigned)tiles), dim3(kGThreads), kLdsBytes,
+                       (hipStream_t)stream, (const uint16_t*)X, (const uint16_t*)W, (uint16_t*)C,
+                       (int)M, (int)N, (int)K);
   return launch_status();
 }
 

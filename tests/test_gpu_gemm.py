@@ -1,6 +1,6 @@
-"""GPU parity of the hand-written MFMA GEMM (mqc_gemm_nt, bf16): ragged M (rows
-past M are clamped for the loads and never stored), several N and K, against
-float64 torch on the same bf16 inputs; and the config-3 B/C projection shape
+"""GPU parity of the hand-written MFMA GEMM (mqc_gemm_nt, bf16 and fp16): ragged M
+(rows past M are clamped for the loads and never stored), several N and K, against
+float64 torch on the same 16-bit inputs; and the config-3 B/C projection shape
 against torch's own GEMM."""
 import pytest
 import torch
@@ -16,22 +16,24 @@ DEV = "cuda"
 def gemm(X, W):
     M, K = X.shape
     N = W.shape[0]
-    C = torch.full((M, N), float("nan"), device=DEV, dtype=torch.bfloat16)
-    nat.call("mqc_gemm_nt", X, X.data_ptr(), W.data_ptr(), C.data_ptr(), M, N, K, nat.BF16,
-             nat.stream_of(X))
+    C = torch.full((M, N), float("nan"), device=DEV, dtype=X.dtype)
+    nat.call("mqc_gemm_nt", X, X.data_ptr(), W.data_ptr(), C.data_ptr(), M, N, K,
+             nat.dtype_code(X), nat.stream_of(X))
     return C
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 256, 64), (5, 512, 128), (255, 256, 192), (257, 768, 1536),
                                    (1000, 1024, 320), (2048, 8192, 1536), (300, 256, 64)])
-def test_gemm_vs_fp64(M, N, K):
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_gemm_vs_fp64(M, N, K, dt):
     g = torch.Generator(device=DEV).manual_seed(M + N + K)
-    X = torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16)
-    W = (torch.randn(N, K, generator=g, device=DEV) * 0.05).to(torch.bfloat16)
+    X = torch.randn(M, K, generator=g, device=DEV).to(dt)
+    W = (torch.randn(N, K, generator=g, device=DEV) * 0.05).to(dt)
     C = gemm(X, W)
+    assert C.dtype == dt
     ref = X.double() @ W.double().t()
-    # One bf16 rounding of an fp32 accumulation: rtol 1e-2 with the atol floor.
-    assert_close(C, ref, 1e-2, f"gemm {M}x{N}x{K}")
+    # One 16-bit rounding of an fp32 accumulation: rtol 1e-2 with the atol floor.
+    assert_close(C, ref, 1e-2, f"gemm {M}x{N}x{K} {dt}")
 
 
 def test_gemm_config3_projection_shape():

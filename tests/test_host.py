@@ -331,8 +331,9 @@ def test_auto_chunk_count_within_the_launch_limit():
 
 def test_gemm_validation_without_gpu():
     lib = nat.load()
-    # bf16 only; N a multiple of 256, K of 64; nothing to do is not an error.
+    # bf16 or fp16; N a multiple of 256, K of 64; nothing to do is not an error.
     assert lib.mqc_gemm_nt(FAKE, FAKE, FAKE, 8, 256, 64, 0, None) == -3
+    assert lib.mqc_gemm_nt(FAKE, FAKE, FAKE, 8, 200, 64, 2, None) == -2  # fp16 reaches the shape check
     assert lib.mqc_gemm_nt(FAKE, FAKE, FAKE, 8, 200, 64, 1, None) == -2
     assert lib.mqc_gemm_nt(FAKE, FAKE, FAKE, 8, 256, 96, 1, None) == -2
     assert lib.mqc_gemm_nt(None, FAKE, FAKE, 8, 256, 64, 1, None) == -1
