@@ -387,8 +387,8 @@ class QuaternionMamba2Block(nn.Module):
 
     fuse_bc (attribute): None runs inference (no autograd) with the B/C
     projections fused into the SSM kernel (ssm_forward_fused_bc) where that
-    kernel applies (bf16 or fp16 without autocast, bias-free projections, d_inner
-    a multiple of 64, even d_state <= 64) and sequences have at least FUSED_BC_MIN_SEQ tokens; True
+    kernel applies (bf16 or fp16 operands, or autocast to either; bias-free
+    projections, d_inner a multiple of 64, even d_state <= 64) and sequences have at least FUSED_BC_MIN_SEQ tokens; True
     also for shorter ones; False never. A forced bc_slice_d takes precedence.
 
     fuse_out (attribute): True runs the output step of bf16 inference (out_proj,
@@ -501,9 +501,12 @@ class QuaternionMamba2Block(nn.Module):
         dt_raw, g_raw = _linear_pair(self.dt_proj, self.gate_proj, x)
         if not recording and self._use_fused_bc(x):
             delta, s = ssm_front(dt_raw, g_raw, x)
-            return ssm_forward_fused_bc(x, self.B_proj.weight, self.C_proj.weight, delta, s,
-                                        self.Lambda_alpha, self.Lambda_imag, self.D, eps=1e-6,
-                                        h0=h0, return_state=return_state)
+            # Under autocast the projections' operands in its dtype, as F.linear casts them.
+            dt = self._gemm_dtype(x)
+            xf, wb, wc = (t if t.dtype == dt else t.to(dt)
+                          for t in (x, self.B_proj.weight, self.C_proj.weight))
+            return ssm_forward_fused_bc(xf, wb, wc, delta, s, self.Lambda_alpha, self.Lambda_imag,
+                                        self.D, eps=1e-6, h0=h0, return_state=return_state)
         if width:
             if recording:
                 if self.B_proj.bias is not None or self.C_proj.bias is not None:
@@ -526,11 +529,11 @@ class QuaternionMamba2Block(nn.Module):
             return False
         if self.B_proj.bias is not None or self.C_proj.bias is not None:
             return False
-        if torch.is_autocast_enabled(x.device.type):
-            return False
         if self.fuse_bc is None and x.shape[1] < FUSED_BC_MIN_SEQ:
             return False
-        return fused_bc_eligible(x, self.B_proj.weight, self.C_proj.weight, self.d_state)
+        dt = (torch.get_autocast_dtype(x.device.type)
+              if torch.is_autocast_enabled(x.device.type) else None)
+        return fused_bc_eligible(x, self.B_proj.weight, self.C_proj.weight, self.d_state, dt)
 
     def _gemm_dtype(self, x: torch.Tensor) -> torch.dtype:
         if torch.is_autocast_enabled(x.device.type):

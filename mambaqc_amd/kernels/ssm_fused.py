@@ -496,15 +496,17 @@ FUSED_BC_SPLIT_MAX_BATCH = 1
 FUSED_BC_SPLIT_WS_MAX = 4 << 30
 
 def fused_bc_eligible(x: torch.Tensor, B_weight: torch.Tensor, C_weight: torch.Tensor,
-                      d_state: int) -> bool:
+                      d_state: int, dtype: torch.dtype | None = None) -> bool:
     """Whether ssm_forward_fused_bc takes these operands: x [batch, T, d_inner] with
     d_inner a multiple of 64 and weights [d_inner * d_state * 4, d_inner] of one shape,
-    all bf16 or all fp16, d_state even and at most 64, all on a ROCm device."""
+    all bf16 or all fp16, d_state even and at most 64, all on a ROCm device. dtype:
+    the type all three will be cast to first (autocast's), or None to take their own."""
     if x.dim() != 3 or not (x.is_cuda and B_weight.is_cuda and C_weight.is_cuda):
         return False
     d_inner = x.shape[-1]
-    return (x.dtype == B_weight.dtype == C_weight.dtype
-            and x.dtype in (torch.bfloat16, torch.float16)
+    dts = (x.dtype, B_weight.dtype, C_weight.dtype) if dtype is None else (dtype,) * 3
+    return (dts[0] == dts[1] == dts[2]
+            and dts[0] in (torch.bfloat16, torch.float16)
             and d_inner % 64 == 0 and 0 < d_state <= 64 and d_state % 2 == 0
             and tuple(B_weight.shape) == tuple(C_weight.shape) == (d_inner * d_state * 4, d_inner))
 

@@ -347,3 +347,28 @@ def test_block_forward_fused_bc_fp16(rows):
     sd = {k: v.detach().float().cpu() for k, v in blk.state_dict().items()}
     want = oracle.block_forward_reference(sd, x.float().cpu(), d_state=64)
     assert_close(got, want, 2e-2, "fp16 block fused vs oracle")
+
+
+@pytest.mark.parametrize("dt", [F16, BF], ids=["f16", "bf16"])
+def test_block_forward_fused_bc_autocast(dt):
+    """fp32 parameters in inference under autocast take the fused path, the
+    projections' operands cast to autocast's dtype as F.linear's would be: against
+    the same block with fusion off under the same autocast, and the CPU oracle of
+    the block in fp32."""
+    import mambaqc_amd
+
+    torch.manual_seed(8)
+    blk = mambaqc_amd.QuaternionMamba2Block(64, d_state=64).to(DEV).eval()
+    g = torch.Generator(device=DEV).manual_seed(9)
+    x = torch.randn(2, 300, 64, generator=g, device=DEV)
+    print(f"autocast {dt} block fused", flush=True)
+    with torch.no_grad(), torch.autocast("cuda", dtype=dt):
+        assert blk._use_fused_bc(torch.empty(2, 300, blk.d_inner, device=DEV, dtype=dt))
+        got = blk(x)
+        blk.fuse_bc = False
+        ref_unfused = blk(x)
+        blk.fuse_bc = None
+    assert_close(got, ref_unfused, 2e-2, f"autocast {dt} block fused vs unfused")
+    sd = {k: v.detach().float().cpu() for k, v in blk.state_dict().items()}
+    want = oracle.block_forward_reference(sd, x.cpu(), d_state=64)
+    assert_close(got, want, 2e-2, f"autocast {dt} block fused vs oracle")
