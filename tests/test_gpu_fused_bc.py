@@ -135,11 +135,12 @@ def test_fused_bc_config3_full_size(dt):
     assert (y_2s.float() - want_2s.float()).abs().max().item() <= 2.0 ** -24
 
 
-def test_fused_bc_state_in_place_and_empty():
+@pytest.mark.parametrize("dt", [BF, F16], ids=["bf16", "f16"])
+def test_fused_bc_state_in_place_and_empty(dt):
     """h_last may be h0 (each (b, d) reads its own states before it writes them),
     through the C ABI; an empty sequence copies h0 to h_last."""
     b, T, d, k = 2, 300, 64, 64
-    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=9)
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=9, dt=dt)
     with torch.no_grad():
         y_ref, h_ref = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0,
                                               return_state=True)
@@ -150,14 +151,14 @@ def test_fused_bc_state_in_place_and_empty():
     st = lib.mqc_ssm_fused_bc_fwd(x.data_ptr(), wb.data_ptr(), wc.data_ptr(), delta.data_ptr(),
                                   s.data_ptr(), la.data_ptr(), li.data_ptr(), D.data_ptr(),
                                   h.data_ptr(), y.data_ptr(), h.data_ptr(), b, T, d, k, 1e-6,
-                                  nat.BF16, stream)
+                                  nat.dtype_code(x), stream)
     assert st == 0, nat.status_string(st)
     torch.cuda.synchronize()
     assert torch.equal(y, y_ref) and torch.equal(h, h_ref)
     h_out = torch.full_like(h0, float("nan"))
     st = lib.mqc_ssm_fused_bc_fwd(None, None, None, None, None, la.data_ptr(), li.data_ptr(),
                                   D.data_ptr(), h0.data_ptr(), None, h_out.data_ptr(), b, 0, d,
-                                  k, 1e-6, nat.BF16, stream)
+                                  k, 1e-6, nat.dtype_code(x), stream)
     assert st == 0, nat.status_string(st)
     torch.cuda.synchronize()
     assert torch.equal(h_out, h0)
@@ -295,14 +296,15 @@ def test_block_batch_of_one_takes_split_fused_path():
     assert_close(one, want, 2e-2, "split fused block vs oracle")
 
 
-def test_fused_bc_split_in_time_segments(monkeypatch):
+@pytest.mark.parametrize("dt", [BF, F16], ids=["bf16", "f16"])
+def test_fused_bc_split_in_time_segments(monkeypatch, dt):
     """A batch of one whose split workspace would pass FUSED_BC_SPLIT_WS_MAX is
     walked in segments of whole 256-token tiles, the fp32 state carried through
     h0 / h_last: the same y and final state as one launch, bit for bit."""
     from mambaqc_amd.kernels import ssm_fused
 
     b, T, d, k = 1, 700, 64, 64
-    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=31)
+    x, wb, wc, delta, s, la, li, D, h0 = _inputs(b, T, d, k, seed=31, dt=dt)
     with torch.no_grad():
         y1, h1 = K.ssm_forward_fused_bc(x, wb, wc, delta, s, la, li, D, h0=h0,
                                         return_state=True, split=False)
