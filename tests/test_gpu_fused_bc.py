@@ -69,6 +69,7 @@ def _oracle(x, wb, wc, delta, s, la, li, D, h0, d_slice, b_slice=slice(None), ep
     (3, 300, 192, 32),   # ragged last tile, one half of states, d_inner 3 x 64
     (1, 77, 64, 16),     # shorter than a tile, a ragged half (16 states)
     (2, 600, 64, 48),    # two halves, the second ragged
+    (1, 300, 64, 34),    # the second half two states (one 8-row DMA group of W rows)
     (1, 1, 128, 2),      # one token, two states
 ])
 @pytest.mark.parametrize("with_h0", [False, True])
@@ -214,6 +215,7 @@ def test_block_forward_fused_bc_path():
 @pytest.mark.parametrize("shape,with_h0", [
     ((1, 300, 128, 64), False),   # ragged last tile, two full halves
     ((1, 600, 64, 48), True),     # the second half ragged (16 states)
+    ((1, 300, 64, 34), True),     # the second half two states
     ((2, 512, 128, 64), True),    # batch 2, state carried across tiles
     ((1, 256, 64, 32), False),    # one half: the split call is the one-launch form
     ((1, 1, 64, 64), True),       # one token
