@@ -36,13 +36,14 @@ def test_gemm_vs_fp64(M, N, K, dt):
     assert_close(C, ref, 1e-2, f"gemm {M}x{N}x{K} {dt}")
 
 
-def test_gemm_config3_projection_shape():
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_gemm_config3_projection_shape(dt):
     """M 8192 (B4 x T2048), N 393216 (d_inner 1536 x d_state 64 x 4), K 1536:
     against torch's GEMM (hipBLASLt) on the same inputs, and row 4321 against
     float64."""
     g = torch.Generator(device=DEV).manual_seed(0)
-    X = torch.randn(8192, 1536, generator=g, device=DEV).to(torch.bfloat16)
-    W = (torch.randn(393216, 1536, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    X = torch.randn(8192, 1536, generator=g, device=DEV).to(dt)
+    W = (torch.randn(393216, 1536, generator=g, device=DEV) * 0.02).to(dt)
     C = gemm(X, W)
     ref = torch.mm(X, W.t())
     err = (C.float() - ref.float()).abs().max().item()
