@@ -146,7 +146,9 @@ def test_lm_base_width_vs_oracle():
 def test_lm_base_config5_forward():
     """Config 5: the base preset (12 layers, d_model 768, d_state 64; 14.66 B
     parameters) in bf16, B4 T2048, vocab 10000. Logits are finite, and causal:
-    changing the last token leaves every earlier position's logits unchanged."""
+    changing the last token leaves every earlier position's logits unchanged; and the
+    blocks' fused B/C path (their default here) agrees with the unfused one through
+    all 12 layers."""
     torch.manual_seed(0)
     with torch.device(DEV):
         lm = mambaqc_amd.quaternion_mamba2_base(10000)
@@ -162,3 +164,13 @@ def test_lm_base_config5_forward():
         logits2 = lm(ids2)["logits"]
     assert_close(logits2[:, :-1], logits[:, :-1], 1e-3, "causality")
     assert (logits2[:, -1] - logits[:, -1]).abs().max() > 0
+    del logits2
+    blocks = [m for m in lm.modules() if isinstance(m, mambaqc_amd.QuaternionMamba2Block)]
+    assert len(blocks) == 12
+    for blk in blocks:
+        blk.fuse_bc = False
+    with torch.inference_mode():
+        unfused = lm(ids)["logits"]
+    for blk in blocks:
+        blk.fuse_bc = None
+    assert_close(logits, unfused, 2e-2, "config 5 logits, fused B/C vs unfused")
